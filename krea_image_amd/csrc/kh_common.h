@@ -1,0 +1,51 @@
+// Shared device/host definitions of the MI355X (gfx950) kernels behind include/kh.h.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/kh.h"
+
+namespace kh {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// ---- 16-bit conversions (round to nearest even, as the reference's bf16(x) / half(x)) ----
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);  // v_cvt_f16_f32: RNE under the default mode
+}
+template <int DT>
+__device__ __forceinline__ uint16_t to16(float f) {
+  return DT == KH_BF16 ? f32_to_bf16_bits(f) : f32_to_f16_bits(f);
+}
+template <int DT>
+__device__ __forceinline__ float from16(uint16_t h) {
+  if (DT == KH_BF16) return __builtin_bit_cast(float, (uint32_t)h << 16);
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+__device__ __forceinline__ float load_scale(const void* s, int s_dtype, size_t i) {
+  if (s_dtype == KH_F16) return (float)((const _Float16*)s)[i];
+  if (s_dtype == KH_BF16) return __builtin_bit_cast(float, (uint32_t)((const uint16_t*)s)[i] << 16);
+  return ((const float*)s)[i];
+}
+
+// ---- epilogue math (engine/kernels/common.h:23-29) ----
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+__device__ __forceinline__ float gelu_tanh_f(float x) {
+  const float k0 = 0.7978845608028654f, k1 = 0.044715f;
+  return 0.5f * x * (1.0f + tanhf(k0 * (x + k1 * x * x * x)));
+}
+
+}  // namespace kh

@@ -1,0 +1,116 @@
+"""Parity of kh_gemm (HIP, through the C ABI) against the CPU oracle's restatement of Metal::gemm.
+
+Tolerance: <= 0.5 % relative L2 per GEMM (the per-GEMM budget of the north star); the fp32-accumulated
+results differ only in summation order, so the measured errors sit far below it.
+"""
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.helpers import from_dev16, make_weight, randn16, rel_l2, to_dev16, weight_to_dev
+
+pytestmark = pytest.mark.gpu
+TOL = 5e-3
+EPIS = ["store16", "f32", "resid_gate", "resid", "swiglu", "gelu", "bias16", "bias_f32"]
+F32_OUT = {"f32", "resid_gate", "resid", "bias_f32"}
+
+
+def run_case(dev, a_dtype, kind, epi, M, N, K, seed=0, rows=None):
+    from krea_image_amd import kh
+    print(f"[gemm case] a_dtype={a_dtype} w={kind} epi={epi} M={M} N={N} K={K} seed={seed}", flush=True)
+    rng = np.random.default_rng(seed)
+    A = randn16(rng, (M, K), a_dtype)
+    wd = make_weight(rng, K, N, kind, a_dtype)
+    vec = rng.standard_normal(N).astype(np.float32) * np.float32(0.1)
+    ncol = N // 2 if epi == "swiglu" else N
+    C0 = rng.standard_normal((M, ncol)).astype(np.float32) if epi in F32_OUT else None
+
+    Ad = to_dev16(A, a_dtype, dev)
+    W = weight_to_dev(wd, dev)
+    vd = torch.from_numpy(vec).to(dev)
+    if epi in F32_OUT:
+        Cd = torch.from_numpy(C0.copy()).to(dev)
+    else:
+        Cd = torch.zeros(M, ncol, dtype=Ad.dtype, device=dev)
+    kh.gemm(epi, Ad, W, Cd, M, N, K, K, N, ncol, vd)
+    torch.cuda.synchronize()
+    got = Cd.cpu().numpy() if epi in F32_OUT else O.to_f32(from_dev16(Cd), a_dtype)
+
+    # oracle on all rows (or a row subset: rows are independent)
+    sel = np.arange(M) if rows is None else rows
+    Cr = None if C0 is None else np.ascontiguousarray(C0[sel])
+    ref = O.gemm(O.EPI[epi], np.ascontiguousarray(A[sel]), a_dtype, wd["w"], wd["w_dtype"], wd["s"], wd["s_dtype"],
+                 wd["group"], C=Cr, vec=vec)
+    ref = ref if epi in F32_OUT else O.to_f32(ref, a_dtype)
+    got = got[sel]
+    if C0 is not None and epi in ("resid", "resid_gate"):  # compare the increments, not the carried residual
+        got, ref = got - C0[sel], ref - C0[sel]
+    err = rel_l2(got, ref)
+    print(f"    rel_l2={err:.3e}", flush=True)
+    assert np.isfinite(got).all()
+    assert err <= TOL, f"rel L2 {err:.3e} > {TOL}"
+    return err
+
+
+@pytest.mark.parametrize("a_dtype", [O.F16, O.BF16])
+@pytest.mark.parametrize("kind", ["ch", "g128", "16"])
+@pytest.mark.parametrize("epi", EPIS)
+def test_gemm_small_all_formats(dev, a_dtype, kind, epi):
+    # M not a multiple of the 256-row tile, N not a multiple of the 256-column tile
+    run_case(dev, a_dtype, kind, epi, M=300, N=320, K=256, seed=zlib.crc32(f"{a_dtype}{kind}{epi}".encode()) % 1000)
+
+
+@pytest.mark.parametrize("M", [1, 7, 64, 257])
+def test_gemm_ragged_rows(dev, M):
+    run_case(dev, O.F16, "ch", "bias16", M=M, N=192, K=128, seed=M)
+
+
+def test_gemm_config1_fp16_bias(dev):
+    """X[4096,3072] fp16 x int8 [3072,3072] per-channel fp16 scales + fp16 bias -> fp16."""
+    run_case(dev, O.F16, "ch", "bias16", M=4096, N=3072, K=3072, seed=1)
+
+
+def test_gemm_mlp_up_full_size_rows(dev):
+    """Target shape M=4096 K=3072 N=12288 with GELU; the oracle checks 96 rows spread over every tile row."""
+    rows = np.sort(np.random.default_rng(5).choice(4096, 96, replace=False))
+    run_case(dev, O.F16, "ch", "gelu", M=4096, N=12288, K=3072, seed=2, rows=rows)
+
+
+def test_gemm_mlp_down_full_size_rows(dev):
+    rows = np.sort(np.random.default_rng(6).choice(4096, 96, replace=False))
+    run_case(dev, O.F16, "ch", "resid", M=4096, N=3072, K=12288, seed=3, rows=rows)
+
+
+def test_gemm_reference_shape_swiglu_g128(dev):
+    """Reference format: bf16 activations, dit_q8 group-128 f32 scales, SwiGLU over interleaved gate|up."""
+    rows = np.sort(np.random.default_rng(7).choice(1024, 64, replace=False))
+    run_case(dev, O.BF16, "g128", "swiglu", M=1024, N=4096, K=6144, seed=4, rows=rows)
+
+
+def test_gemm_strided_output(dev):
+    """lda / ldc larger than the logical widths (the reference writes q|k|v|gate column slices)."""
+    from krea_image_amd import kh
+    rng = np.random.default_rng(11)
+    M, N, K, lda, ldc = 200, 128, 192, 256, 512
+    A = randn16(rng, (M, lda), O.F16)
+    wd = make_weight(rng, K, N, "ch", O.F16)
+    Ad = to_dev16(A, O.F16, dev)
+    Cd = torch.zeros(M, ldc, dtype=torch.float16, device=dev)
+    kh.gemm("store16", Ad, weight_to_dev(wd, dev), Cd[:, 64:], M, N, K, lda, N, ldc)
+    torch.cuda.synchronize()
+    got = O.to_f32(from_dev16(Cd), O.F16)
+    ref = O.to_f32(O.gemm(0, np.ascontiguousarray(A[:, :K]), O.F16, wd["w"], O.I8, wd["s"], O.F16, K), O.F16)
+    assert rel_l2(got[:, 64:64 + N], ref) <= TOL
+    assert not got[:, :64].any() and not got[:, 64 + N:].any(), "columns outside [64, 64+N) were written"
+
+
+def test_gemm_rejects_bad_shapes(dev):
+    from krea_image_amd import kh
+    A = torch.zeros(64, 96, dtype=torch.float16, device=dev)
+    W = kh.Weight(torch.zeros(96, 64, dtype=torch.int8, device=dev), torch.ones(64, dtype=torch.float16, device=dev))
+    C = torch.zeros(64, 64, dtype=torch.float16, device=dev)
+    with pytest.raises(kh.KhError, match="K % 64"):
+        kh.gemm("store16", A, W, C, 64, 64, 96, 96, 64, 64)
