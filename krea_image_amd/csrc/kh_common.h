@@ -47,5 +47,16 @@ __device__ __forceinline__ float gelu_tanh_f(float x) {
   const float k0 = 0.7978845608028654f, k1 = 0.044715f;
   return 0.5f * x * (1.0f + tanhf(k0 * (x + k1 * x * x * x)));
 }
+// Epilogue forms on the hardware exp / reciprocal (v_exp_f32, v_rcp_f32, ~1 ulp each):
+//   gelu_tanh(x) = 0.5 x (1 + tanh(u)) = x / (1 + e^(-2u)),  u = k0 (x + k1 x^3)
+//   silu(x) = x / (1 + e^(-x))
+// Both saturate correctly: e^(...) -> inf gives -0, e^(...) -> 0 gives x.
+__device__ __forceinline__ float rcp_fast(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float gelu_fast(float x) {
+  const float k0 = 0.7978845608028654f, k1 = 0.044715f;
+  const float u = k0 * (x + k1 * x * x * x);
+  return x * rcp_fast(1.0f + __expf(-2.0f * u));
+}
+__device__ __forceinline__ float silu_fast(float x) { return x * rcp_fast(1.0f + __expf(-x)); }
 
 }  // namespace kh

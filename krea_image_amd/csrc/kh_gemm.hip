@@ -26,6 +26,8 @@
 //  * Tile order: block ids are first made contiguous per XCD (the dispatcher deals workgroups round-robin
 //    to the 8 XCDs, each with its own L2), then walked in groups of 8 tile rows, so co-resident
 //    workgroups of one XCD share both X row panels and W column panels in that XCD's L2.
+#include <type_traits>
+
 #include "kh_common.h"
 #include "kh_internal.h"
 
@@ -33,8 +35,13 @@ namespace kh {
 
 namespace {
 
-constexpr int BM = 256, BN = 256, BK = 64, NTHR = 512;
-constexpr int TILE = BM * BK;  // 16-bit elements of one X (or W) tile
+constexpr int BM = 256, BN = 256, BK = 64;
+#ifndef KH_GEMM_WAVES
+#define KH_GEMM_WAVES 8
+#endif
+constexpr int WAVES_DEFAULT = KH_GEMM_WAVES;
+constexpr int STAGE = BM * BK * 2;  // bytes of one 16-bit 256 x 64 tile
+constexpr int X_STAGES = 3, W_STAGES = 2;
 constexpr int GROUP_M = 8;
 
 enum { WF_16 = 0, WF_I8_CHANNEL = 1, WF_I8_GROUP = 2 };
@@ -48,6 +55,20 @@ struct GemmArgs {
   int M, N, K, lda, ldw, ldc, group, s_dtype;
 };
 
+// 16-byte chunk XOR of LDS row `row` (rows are 128 bytes = 8 chunks of 8 k). Depends on row & 31 only, is a
+// bijection on any 8 consecutive rows (operand reads: 32 consecutive rows per instruction) and on rows
+// {j, j+4, ..., j+28} (the weight writes: lane L writes row 4L + j).
+__device__ __forceinline__ int swz(int row) { return (row ^ (row >> 2)) & 7; }
+
+// s_waitcnt immediate (gfx9 encoding): vmcnt <= vm, lgkmcnt <= lgkm, expcnt untouched.
+__host__ __device__ constexpr int waitcnt_imm(int vm, int lgkm) {
+  return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | (lgkm << 8);
+}
+
+// Workgroup barrier that is also a compiler memory barrier, without the release fence of __syncthreads
+// (which would wait for the activation tiles still streaming into LDS for later K steps).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 template <int ACT>
 __device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, const f32x16& c) {
   if constexpr (ACT == KH_BF16)
@@ -58,89 +79,90 @@ __device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, const f
                                                   0);
 }
 
-// Weight registers of one thread for one K step: 8 k-rows x 4 n-columns.
-template <int WF>
-struct WRegs;
-template <>
-struct WRegs<WF_16> {
-  u32x2 r[8];
-};
-template <>
-struct WRegs<WF_I8_CHANNEL> {
-  uint32_t r[8];
-};
-template <>
-struct WRegs<WF_I8_GROUP> {
-  uint32_t r[8];
+// Raw weight registers of one thread for one K step: KR k-rows x 4 n-columns (+ the 4 column scales).
+template <int WF, int KR>
+struct WRaw {
+  uint32_t r[KR];
   float s[4];
 };
+template <int KR>
+struct WRaw<WF_16, KR> {
+  u32x2 r[KR];
+};
 
-template <int ACT, int WF>
-__device__ __forceinline__ void convert_w(const WRegs<WF>& w, u32x4 (&out)[4]) {
+// Convert k-rows [8h, 8h+8) of column j to one 16-byte vector of 8 consecutive k (16-bit each).
+template <int ACT, int WF, int KR>
+__device__ __forceinline__ u32x4 convert_chunk(const WRaw<WF, KR>& w, int j, int h) {
+  u32x4 out;
   if constexpr (WF == WF_16) {
-    // halfword j of rows 2p (low) and 2p + 1 (high)
+    const uint32_t jj = (j & 1) * 2;
+    const uint32_t sel = jj | ((jj + 1) << 8) | ((jj + 4) << 16) | ((jj + 5) << 24);
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const uint32_t jj = (j & 1) * 2;
-      const uint32_t sel = (jj) | ((jj + 1) << 8) | ((jj + 4) << 16) | ((jj + 5) << 24);
-#pragma unroll
-      for (int p = 0; p < 4; p++) {
-        const uint32_t lo = (j < 2) ? w.r[2 * p].x : w.r[2 * p].y;
-        const uint32_t hi = (j < 2) ? w.r[2 * p + 1].x : w.r[2 * p + 1].y;
-        out[j][p] = __builtin_amdgcn_perm(hi, lo, sel);
-      }
+    for (int p = 0; p < 4; p++) {
+      const uint32_t lo = (j < 2) ? w.r[8 * h + 2 * p].x : w.r[8 * h + 2 * p].y;
+      const uint32_t hi = (j < 2) ? w.r[8 * h + 2 * p + 1].x : w.r[8 * h + 2 * p + 1].y;
+      out[p] = __builtin_amdgcn_perm(hi, lo, sel);
     }
   } else if constexpr (WF == WF_I8_CHANNEL && ACT == KH_F16) {
+    // 0x6400 | (q ^ 0x80) is the fp16 number 1024 + q + 128: one packed subtract of 1152 gives q exactly
+    const uint32_t sel = (uint32_t)j | (0x0cu << 8) | ((uint32_t)(4 + j) << 16) | (0x0cu << 24);
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const uint32_t sel = (uint32_t)j | (0x0cu << 8) | ((uint32_t)(4 + j) << 16) | (0x0cu << 24);
-#pragma unroll
-      for (int p = 0; p < 4; p++) {
-        const uint32_t d = __builtin_amdgcn_perm(w.r[2 * p + 1], w.r[2 * p], sel) ^ 0x64806480u;
-        const f16x2 h = __builtin_bit_cast(f16x2, d) - (f16x2){(_Float16)1152.0f, (_Float16)1152.0f};
-        out[j][p] = __builtin_bit_cast(uint32_t, h);
-      }
+    for (int p = 0; p < 4; p++) {
+      const uint32_t d = __builtin_amdgcn_perm(w.r[8 * h + 2 * p + 1], w.r[8 * h + 2 * p], sel) ^ 0x64806480u;
+      const f16x2 v = __builtin_bit_cast(f16x2, d) - (f16x2){(_Float16)1152.0f, (_Float16)1152.0f};
+      out[p] = __builtin_bit_cast(uint32_t, v);
     }
-  } else if constexpr (WF == WF_I8_CHANNEL) {  // bf16 activations
-    uint32_t r[8];
+  } else if constexpr (WF == WF_I8_CHANNEL) {
+    // bf16: the f32 2^23 + (q ^ 0x80) minus 2^23 + 128 is q exactly; its upper half is its bf16 encoding
+    const uint32_t sel = (uint32_t)j | (0x0cu << 8) | (0x0cu << 16) | (7u << 24);
 #pragma unroll
-    for (int i = 0; i < 8; i++) r[i] = w.r[i] ^ 0x80808080u;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const uint32_t sel = (uint32_t)j | (0x0cu << 8) | (0x0cu << 16) | (7u << 24);
-#pragma unroll
-      for (int p = 0; p < 4; p++) {
-        const float lo = __builtin_bit_cast(float, __builtin_amdgcn_perm(0x4b000000u, r[2 * p], sel)) - 8388736.0f;
-        const float hi = __builtin_bit_cast(float, __builtin_amdgcn_perm(0x4b000000u, r[2 * p + 1], sel)) - 8388736.0f;
-        out[j][p] = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, hi), __builtin_bit_cast(uint32_t, lo),
-                                          0x07060302u);
-      }
+    for (int p = 0; p < 4; p++) {
+      const uint32_t a = w.r[8 * h + 2 * p] ^ 0x80808080u, b = w.r[8 * h + 2 * p + 1] ^ 0x80808080u;
+      const float lo = __builtin_bit_cast(float, __builtin_amdgcn_perm(0x4b000000u, a, sel)) - 8388736.0f;
+      const float hi = __builtin_bit_cast(float, __builtin_amdgcn_perm(0x4b000000u, b, sel)) - 8388736.0f;
+      out[p] = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, hi), __builtin_bit_cast(uint32_t, lo), 0x07060302u);
     }
-  } else {  // WF_I8_GROUP: round16(q * s), single f32 rounding of the product
-    uint32_t r[8];
+  } else {
+    // group scales: round16(q * s) with the product rounded once in f32: fma(q + 128, s, -128 s)
+    const float s = w.s[j], nb = -128.0f * w.s[j];
 #pragma unroll
-    for (int i = 0; i < 8; i++) r[i] = w.r[i] ^ 0x80808080u;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const float s = w.s[j], nb = -128.0f * w.s[j];
-#pragma unroll
-      for (int p = 0; p < 4; p++) {
-        const float lo = __builtin_fmaf((float)((r[2 * p] >> (8 * j)) & 0xffu), s, nb);
-        const float hi = __builtin_fmaf((float)((r[2 * p + 1] >> (8 * j)) & 0xffu), s, nb);
-        out[j][p] = (uint32_t)to16<ACT>(lo) | ((uint32_t)to16<ACT>(hi) << 16);
-      }
+    for (int p = 0; p < 4; p++) {
+      const uint32_t a = w.r[8 * h + 2 * p] ^ 0x80808080u, b = w.r[8 * h + 2 * p + 1] ^ 0x80808080u;
+      const float lo = __builtin_fmaf((float)((a >> (8 * j)) & 0xffu), s, nb);
+      const float hi = __builtin_fmaf((float)((b >> (8 * j)) & 0xffu), s, nb);
+      out[p] = (uint32_t)to16<ACT>(lo) | ((uint32_t)to16<ACT>(hi) << 16);
     }
   }
+  return out;
 }
 
-template <int ACT, int WF, int EPI>
-__global__ __launch_bounds__(NTHR) void gemm_kernel(GemmArgs p) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2][2 * TILE];
+// Wave layout of a 256 x 256 block tile with WAVES wave64s: a 2 (n) x WAVES/2 (m) grid, each wave owning
+// 128 n x WME m = 4 x IB blocks of 32 x 32. WAVES = 8 runs two waves per SIMD (128 accumulators each), so
+// one wave's LDS / memory waits are covered by the other wave's MFMAs.
+template <int WAVES>
+struct Cfg {
+  static constexpr int NTHR = 64 * WAVES;
+  static constexpr int WME = BM / (WAVES / 2);  // m extent of a wave
+  static constexpr int IB = WME / 32;           // 32-row MFMA blocks per wave
+  static constexpr int X_LOADS = 32 / WAVES;    // 1 KB LDS-direct activation loads per thread per K step
+  static constexpr int KR = BK / WAVES;         // weight k-rows loaded per thread per K step
+  static constexpr int WCH = 4 * (KR / 8);      // converted 16-byte weight chunks per thread per K step
+  // loads issued per thread per K step, counted in the waits (a lower bound when group scales are loaded)
+  static constexpr int LOADS = X_LOADS + KR;
+};
+
+template <int ACT, int WF, int EPI, int WAVES>
+__global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
+  using C_ = Cfg<WAVES>;
+  constexpr int NTHR = C_::NTHR, IB = C_::IB, X_LOADS = C_::X_LOADS, KR = C_::KR, WCH = C_::WCH;
+  // [X stage 0 | X stage 1 | X stage 2 | W stage 0 | W stage 1], 32 KB each
+  __shared__ __attribute__((aligned(1024))) char lds[(X_STAGES + W_STAGES) * STAGE];
+  typedef __attribute__((address_space(3))) void lds_void;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
   // ---- tile order (XCD-contiguous, then grouped by GROUP_M tile rows) ----
-  const int tiles_n = p.N / BN + (p.N % BN ? 1 : 0), tiles_m = (p.M + BM - 1) / BM;
+  const int tiles_n = (p.N + BN - 1) / BN, tiles_m = (p.M + BM - 1) / BM;
   const int total = tiles_n * tiles_m;
   int pid = blockIdx.x;
   if (total % 8 == 0) pid = (pid % 8) * (total / 8) + pid / 8;
@@ -150,168 +172,226 @@ __global__ __launch_bounds__(NTHR) void gemm_kernel(GemmArgs p) {
   const int in_g = pid % group_sz;
   const int m0 = (first_m + in_g % gm) * BM, n0 = (in_g / gm) * BN;
 
-  // ---- X tile: 4 chunks of 16 B per thread (8 lanes per 128-byte row) ----
-  const uint16_t* a_src[4];
-  int a_lds[4];
+  // ---- X tile (activations) -> LDS directly: instruction r of wave w fills 1 KB block b = WAVES r + w,
+  //      i.e. rows 8 WAVES r + 8w + lane/8; lane slot lane & 7 receives logical chunk (lane & 7) ^ swz(row)
+  //      (swz of those rows does not depend on r) ----
+  const int xrow0 = wave * 8 + (lane >> 3);
+  const int xchunk = ((lane & 7) ^ swz(xrow0)) * 8;
+  int xoff[X_LOADS];
 #pragma unroll
-  for (int r = 0; r < 4; r++) {
-    const int cid = tid + r * NTHR, row = cid >> 3, ch = cid & 7;
-    const int grow = min(m0 + row, p.M - 1);  // rows >= M are computed from row M-1, never stored
-    a_src[r] = (const uint16_t*)p.A + (size_t)grow * p.lda + ch * 8;
-    a_lds[r] = row * BK + ((ch ^ (row & 7)) * 8);
-  }
-  // ---- W tile: k-rows wave*8 .. +7, columns n0 + lane*4 .. +3 ----
-  const int wcol = min(n0 + lane * 4, p.N - 4);  // columns >= N (partial last tile) are never stored
-  const size_t wrow_bytes = (size_t)p.ldw * (WF == WF_16 ? 2 : 1);
-  const char* w_src = (const char*)p.W + (size_t)(wave * 8) * wrow_bytes + (size_t)wcol * (WF == WF_16 ? 2 : 1);
-  int w_lds[4];
+  for (int r = 0; r < X_LOADS; r++) xoff[r] = min(m0 + 8 * WAVES * r + xrow0, p.M - 1) * p.lda + xchunk;
+  const uint16_t* xbase = (const uint16_t*)p.A;
+  auto issue_x_to = [&](int t, int stage) {
+    char* dst = lds + stage * STAGE + wave * 1024;
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const int nl = lane * 4 + j;
-    w_lds[j] = TILE + nl * BK + ((wave ^ (nl & 7)) * 8);
-  }
+    for (int r = 0; r < X_LOADS; r++)
+      __builtin_amdgcn_global_load_lds((const void*)(xbase + xoff[r] + t * BK), (lds_void*)(dst + r * WAVES * 1024),
+                                       16, 0, 0);
+  };
 
-  u32x4 ra[4];
-  WRegs<WF> rw;
-  auto load_step = [&](int t) {
-    const int k0 = t * BK;
+  // ---- W tile: wave w loads k-rows [KR w, KR w + KR), lane columns n0 + 4 lane .. + 3 ----
+  const int wcol = min(n0 + lane * 4, p.N - 4);  // columns >= N (last tile) are never stored
+  constexpr int WB = (WF == WF_16) ? 2 : 1;
+  const char* wbase = (const char*)p.W + ((size_t)(wave * KR) * p.ldw + wcol) * WB;
+  const size_t wrow = (size_t)p.ldw * WB;
+  auto issue_w = [&](int t, WRaw<WF, KR>& R) {
+    const char* src = wbase + (size_t)(t * BK) * wrow;
 #pragma unroll
-    for (int r = 0; r < 4; r++) ra[r] = *(const u32x4*)(a_src[r] + k0);
-    const char* ws = w_src + (size_t)k0 * wrow_bytes;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
+    for (int i = 0; i < KR; i++) {
       if constexpr (WF == WF_16)
-        rw.r[i] = *(const u32x2*)(ws + (size_t)i * wrow_bytes);
+        R.r[i] = *(const u32x2*)(src + i * wrow);
       else
-        rw.r[i] = *(const uint32_t*)(ws + (size_t)i * wrow_bytes);
+        R.r[i] = *(const uint32_t*)(src + i * wrow);
     }
     if constexpr (WF == WF_I8_GROUP) {
-      const size_t g = (size_t)(k0 / p.group) * p.ldw + wcol;
+      const size_t g = (size_t)((t * BK) / p.group) * p.ldw + wcol;
 #pragma unroll
-      for (int j = 0; j < 4; j++) rw.s[j] = load_scale(p.S, p.s_dtype, g + j);
+      for (int j = 0; j < 4; j++) R.s[j] = load_scale(p.S, p.s_dtype, g + j);
     }
   };
-  auto store_step = [&](int buf) {
-    uint16_t* L = lds[buf];
+  constexpr int H = KR / 8;  // k-chunks (8 rows) per column and thread
+  int woff[WCH];  // LDS byte offsets of this thread's converted chunks (column j, half h) in a W stage
 #pragma unroll
-    for (int r = 0; r < 4; r++) *(u32x4*)(L + a_lds[r]) = ra[r];
-    u32x4 wv[4];
-    convert_w<ACT, WF>(rw, wv);
+  for (int j = 0; j < 4; j++)
 #pragma unroll
-    for (int j = 0; j < 4; j++) *(u32x4*)(L + w_lds[j]) = wv[j];
+    for (int h = 0; h < H; h++) {
+      const int nl = lane * 4 + j;
+      woff[j * H + h] = nl * 128 + (((H * wave + h) ^ swz(nl)) * 16);
+    }
+  auto store_w = [&](const WRaw<WF, KR>& R, int stage, int q) {  // quarter q of the thread's chunks
+    char* base = lds + (X_STAGES + stage) * STAGE;
+#pragma unroll
+    for (int c = q * WCH / 4; c < (q + 1) * WCH / 4; c++)
+      *(u32x4*)(base + woff[c]) = convert_chunk<ACT, WF, KR>(R, c / H, c % H);
   };
 
-  // ---- MFMA operand addressing: wave (wn, wm) owns n [wn*64, +64), m [wm*128, +128) ----
-  const int wn = wave & 3, wm = wave >> 2;
+  // ---- MFMA operands: wave (wn, wm) owns n [128 wn, +128) x m [WME wm, +WME) = 4 x IB blocks of 32 x 32 ----
+  const int wn = wave & 1, wm = wave >> 1;
   const int l32 = lane & 31, khalf = lane >> 5;
-  const int w_frag = TILE + (wn * 64 + l32) * BK;
-  const int x_frag = (wm * 128 + l32) * BK;
+  const int w_rd = (wn * 128 + l32) * 128, x_rd = (wm * C_::WME + l32) * 128;
+  int sw[4];
+#pragma unroll
+  for (int s = 0; s < 4; s++) sw[s] = (((2 * s + khalf) ^ swz(l32)) * 16);
 
-  f32x16 acc[2][4];
+  f32x16 acc[4][IB];
 #pragma unroll
-  for (int jb = 0; jb < 2; jb++)
+  for (int jb = 0; jb < 4; jb++)
 #pragma unroll
-    for (int ib = 0; ib < 4; ib++) acc[jb][ib] = (f32x16){};
+    for (int ib = 0; ib < IB; ib++) acc[jb][ib] = (f32x16){};
+
+  auto read_frags = [&](const char* xs, const char* ws, int s, u32x4 (&wf)[4], u32x4 (&xf)[IB]) {
+#pragma unroll
+    for (int jb = 0; jb < 4; jb++) wf[jb] = *(const u32x4*)(ws + w_rd + jb * 32 * 128 + sw[s]);
+#pragma unroll
+    for (int ib = 0; ib < IB; ib++) xf[ib] = *(const u32x4*)(xs + x_rd + ib * 32 * 128 + sw[s]);
+  };
 
   const int nk = p.K / BK;
-  load_step(0);
-  store_step(0);
-  __syncthreads();
-  for (int t = 0; t < nk; t++) {
-    const int cur = t & 1;
-    if (t + 1 < nk) load_step(t + 1);
-    const uint16_t* L = lds[cur];
-#pragma unroll
-    for (int s = 0; s < BK / 16; s++) {
-      const int sw = ((s * 2 + khalf) ^ (lane & 7)) * 8;
-      u32x4 wf[2], xf[4];
-#pragma unroll
-      for (int jb = 0; jb < 2; jb++) wf[jb] = *(const u32x4*)(L + w_frag + jb * 32 * BK + sw);
-#pragma unroll
-      for (int ib = 0; ib < 4; ib++) xf[ib] = *(const u32x4*)(L + x_frag + ib * 32 * BK + sw);
-#pragma unroll
-      for (int jb = 0; jb < 2; jb++)
-#pragma unroll
-        for (int ib = 0; ib < 4; ib++) acc[jb][ib] = mfma32<ACT>(wf[jb], xf[ib], acc[jb][ib]);
-    }
-    if (t + 1 < nk) store_step(cur ^ 1);
-    __syncthreads();
-  }
+  constexpr int LOADS = C_::LOADS;
 
-  // ---- epilogue: lane holds, per (jb, ib), row m = m0 + wm*128 + ib*32 + l32 and columns
-  //      n = n0 + wn*64 + jb*32 + g*8 + khalf*4 + e  (g = 0..3, e = 0..3) in acc[jb][ib][g*4 + e] ----
-  const bool per_channel = (WF == WF_I8_CHANNEL);
+  // One K step: multiply stage t; convert raw(t + 1) into the other W stage between the MFMAs; the loads
+  // of step t + 2 (activations straight into LDS, weights into Rl) are in flight meanwhile. Every step is
+  // the same code: past the last step the loads re-fetch step nk - 1 into buffers nobody reads (stage
+  // (t + 2) % 3 and the W stage of t + 1 are never the stage being multiplied), so the loop has no branches.
+  auto step = [&](int t, const WRaw<WF, KR>& Rc, WRaw<WF, KR>& Rl) {
+    const int tl = min(t + 2, nk - 1);
+    issue_x_to(tl, (t + 2) % X_STAGES);
+    issue_w(tl, Rl);
+    const char* xs = lds + (t % X_STAGES) * STAGE;
+    const char* ws = lds + (X_STAGES + (t & 1)) * STAGE;
+    u32x4 wf[2][4], xf[2][IB];
+    read_frags(xs, ws, 0, wf[0], xf[0]);
 #pragma unroll
-  for (int jb = 0; jb < 2; jb++) {
-    if (EPI == KH_EPI_SWIGLU && jb == 1) break;
+    for (int s = 0; s < 4; s++) {
+      if (s < 3) read_frags(xs, ws, s + 1, wf[(s + 1) & 1], xf[(s + 1) & 1]);
 #pragma unroll
-    for (int g = 0; g < 4; g++) {
-      const int n = n0 + wn * 64 + jb * 32 + g * 8 + khalf * 4;
-      if (n >= p.N) continue;
-      float sc[4] = {1.f, 1.f, 1.f, 1.f}, sc_up[4] = {1.f, 1.f, 1.f, 1.f}, vv[4] = {0.f, 0.f, 0.f, 0.f};
-      if (per_channel) {
+      for (int jb = 0; jb < 4; jb++)
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          sc[e] = load_scale(p.S, p.s_dtype, n + e);
-          if (EPI == KH_EPI_SWIGLU) sc_up[e] = load_scale(p.S, p.s_dtype, n + 32 + e);
-        }
-      }
-      if (EPI == KH_EPI_RESID_GATE || EPI == KH_EPI_BIAS16 || EPI == KH_EPI_BIAS_F32) {
-        const f32x4 v4 = *(const f32x4*)(p.vec + n);
+        for (int ib = 0; ib < IB; ib++) acc[jb][ib] = mfma32<ACT>(wf[s & 1][jb], xf[s & 1][ib], acc[jb][ib]);
+      store_w(Rc, (t + 1) & 1, s);
+    }
+    // activations of step t + 1 must have landed: only this step's loads may still be outstanding
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(LOADS, 15));
+    lds_barrier();
+  };
+
+  WRaw<WF, KR> R0, R1;
+  issue_x_to(0, 0);
+  issue_w(0, R0);
+  issue_x_to(min(1, nk - 1), 1);
+  issue_w(min(1, nk - 1), R1);
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(LOADS, 15));
 #pragma unroll
-        for (int e = 0; e < 4; e++) vv[e] = v4[e];
-      }
+  for (int q = 0; q < 4; q++) store_w(R0, 0, q);
+  lds_barrier();
+  int t = 0;
+  for (; t + 1 < nk; t += 2) {
+    step(t, R1, R0);
+    step(t + 1, R0, R1);
+  }
+  if (t < nk) step(t, R1, R0);
+  // the re-fetches issued by the last steps must land before the LDS is reused below
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
+  lds_barrier();
+
+  // ---- epilogue. The LDS is free after the last barrier: the block's 256 column scales and vec entries
+  //      are staged as f32, then the finished values are staged row-major and written out (or, for the
+  //      residual epilogues, read-modify-written) with 16-byte vectors covering whole rows of the tile.
+  //      Per (jb, ib) the lane holds row m = WME wm + 32 ib + l32 and columns
+  //      n = 128 wn + 32 jb + 8 g + 4 khalf + e (g, e = 0..3) of the tile in acc[jb][ib][4 g + e]. ----
+  constexpr bool OUT16 = (EPI == KH_EPI_STORE16 || EPI == KH_EPI_GELU || EPI == KH_EPI_BIAS16 || EPI == KH_EPI_SWIGLU);
+  constexpr bool HAS_VEC = (EPI == KH_EPI_RESID_GATE || EPI == KH_EPI_BIAS16 || EPI == KH_EPI_BIAS_F32);
+  constexpr int OUT_COLS = (EPI == KH_EPI_SWIGLU) ? BN / 2 : BN;
+  constexpr int ELEM = OUT16 ? 2 : 4;
+  constexpr int ROW_BYTES = OUT_COLS * ELEM + 16;             // padded staging row
+  constexpr int PASS_ROWS = OUT16 ? BM : BM / 2;              // f32 tiles go out in two row halves
+  constexpr int SC_OFF = PASS_ROWS * ROW_BYTES;
+  static_assert(SC_OFF + 2 * BN * 4 <= (X_STAGES + W_STAGES) * STAGE, "epilogue staging exceeds LDS");
+  float* sc_l = (float*)(lds + SC_OFF);
+  float* vv_l = sc_l + BN;
+  if (tid < BN) {
+    const int n = n0 + tid;
+    float sv = 1.f, vv = 0.f;
+    if (n < p.N) {
+      if (WF == WF_I8_CHANNEL) sv = load_scale(p.S, p.s_dtype, n);
+      if (HAS_VEC) vv = p.vec[n];
+    }
+    sc_l[tid] = sv;
+    vv_l[tid] = vv;
+  }
+  lds_barrier();
+
+  const int out_n0 = (EPI == KH_EPI_SWIGLU) ? n0 / 2 : n0;
+  const int out_N = (EPI == KH_EPI_SWIGLU) ? p.N / 2 : p.N;
 #pragma unroll
-      for (int ib = 0; ib < 4; ib++) {
-        const int m = m0 + wm * 128 + ib * 32 + l32;
-        if (m >= p.M) continue;
-        float v[4];
+  for (int pass = 0; pass < BM / PASS_ROWS; pass++) {
+    if (PASS_ROWS == BM || (wm * C_::WME) / PASS_ROWS == pass) {
+      const int row_base = wm * C_::WME - pass * PASS_ROWS;
 #pragma unroll
-        for (int e = 0; e < 4; e++) v[e] = acc[jb][ib][g * 4 + e] * sc[e];
-        if constexpr (EPI == KH_EPI_SWIGLU) {
-          uint16_t h[4];
+      for (int jb = 0; jb < 4; jb++) {
+        if (EPI == KH_EPI_SWIGLU && (jb & 1)) continue;  // up blocks are consumed with their gate block
 #pragma unroll
-          for (int e = 0; e < 4; e++) h[e] = to16<ACT>(silu_f(v[e]) * (acc[1][ib][g * 4 + e] * sc_up[e]));
-          const int col = (n / 64) * 32 + (n % 32);
-          *(u32x2*)((uint16_t*)p.C + (size_t)m * p.ldc + col) =
-              (u32x2){(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16)};
-        } else if constexpr (EPI == KH_EPI_STORE16 || EPI == KH_EPI_GELU || EPI == KH_EPI_BIAS16) {
-          uint16_t h[4];
+        for (int g = 0; g < 4; g++) {
+          const int nl = wn * 128 + jb * 32 + g * 8 + khalf * 4;  // tile column of e = 0
+          const f32x4 sc = *(const f32x4*)(sc_l + nl);
+          f32x4 sc_up = sc, vv = {};
+          if (EPI == KH_EPI_SWIGLU) sc_up = *(const f32x4*)(sc_l + nl + 32);
+          if (HAS_VEC) vv = *(const f32x4*)(vv_l + nl);
+          const int ol = (EPI == KH_EPI_SWIGLU) ? (nl / 64) * 32 + (nl % 32) : nl;  // staged column
 #pragma unroll
-          for (int e = 0; e < 4; e++) {
-            float o = v[e];
-            if (EPI == KH_EPI_GELU) o = gelu_tanh_f(o);
-            if (EPI == KH_EPI_BIAS16) o += vv[e];
-            h[e] = to16<ACT>(o);
+          for (int ib = 0; ib < IB; ib++) {
+            char* dst = lds + (row_base + ib * 32 + l32) * ROW_BYTES + ol * ELEM;
+            float o[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+              const float v = acc[jb][ib][g * 4 + e] * sc[e];
+              if (EPI == KH_EPI_SWIGLU) o[e] = silu_fast(v) * (acc[jb + 1][ib][g * 4 + e] * sc_up[e]);
+              else if (EPI == KH_EPI_GELU) o[e] = gelu_fast(v);
+              else if (EPI == KH_EPI_BIAS16 || EPI == KH_EPI_BIAS_F32) o[e] = v + vv[e];
+              else if (EPI == KH_EPI_RESID_GATE) o[e] = v * vv[e];
+              else o[e] = v;
+            }
+            if constexpr (OUT16)
+              *(u32x2*)dst = (u32x2){(uint32_t)to16<ACT>(o[0]) | ((uint32_t)to16<ACT>(o[1]) << 16),
+                                     (uint32_t)to16<ACT>(o[2]) | ((uint32_t)to16<ACT>(o[3]) << 16)};
+            else
+              *(f32x4*)dst = (f32x4){o[0], o[1], o[2], o[3]};
           }
-          *(u32x2*)((uint16_t*)p.C + (size_t)m * p.ldc + n) =
-              (u32x2){(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16)};
-        } else {
-          f32x4* dst = (f32x4*)((float*)p.C + (size_t)m * p.ldc + n);
-          f32x4 o;
-          if (EPI == KH_EPI_RESID_GATE || EPI == KH_EPI_RESID) o = *dst;
-#pragma unroll
-          for (int e = 0; e < 4; e++) {
-            if (EPI == KH_EPI_F32) o[e] = v[e];
-            else if (EPI == KH_EPI_BIAS_F32) o[e] = v[e] + vv[e];
-            else if (EPI == KH_EPI_RESID) o[e] += v[e];
-            else o[e] += vv[e] * v[e];
-          }
-          *dst = o;
         }
       }
     }
+    lds_barrier();
+    // copy-out: 16-byte chunks, CPR per staged row, consecutive threads along a row
+    constexpr int CPR = OUT_COLS * ELEM / 16;
+    constexpr int CHUNKS = PASS_ROWS * CPR;
+    const int grow0 = m0 + pass * PASS_ROWS;
+#pragma unroll 4
+    for (int idx = tid; idx < CHUNKS; idx += NTHR) {
+      const int r = idx / CPR, c = idx % CPR;
+      const int gm_ = grow0 + r, gcol = out_n0 + c * (16 / ELEM);
+      if (gm_ >= p.M || gcol >= out_N) continue;
+      const u32x4 v = *(const u32x4*)(lds + r * ROW_BYTES + c * 16);
+      char* gp = (char*)p.C + ((size_t)gm_ * p.ldc + gcol) * ELEM;
+      if constexpr (EPI == KH_EPI_RESID || EPI == KH_EPI_RESID_GATE) {
+        f32x4 x = *(const f32x4*)gp;
+        x += __builtin_bit_cast(f32x4, v);
+        *(f32x4*)gp = x;
+      } else {
+        *(u32x4*)gp = v;
+      }
+    }
+    if (pass + 1 < BM / PASS_ROWS) lds_barrier();
   }
 }
 
 template <int ACT, int WF>
 hipError_t launch_epi(int epi, const GemmArgs& a, hipStream_t st) {
   const int tiles = ((a.N + BN - 1) / BN) * ((a.M + BM - 1) / BM);
-  dim3 grid(tiles), block(NTHR);
+  dim3 grid(tiles), block(64 * WAVES_DEFAULT);
   switch (epi) {
 #define KH_CASE(E)                                                        \
   case E:                                                                 \
-    hipLaunchKernelGGL((gemm_kernel<ACT, WF, E>), grid, block, 0, st, a); \
+    hipLaunchKernelGGL((gemm_kernel<ACT, WF, E, WAVES_DEFAULT>), grid, block, 0, st, a); \
     break;
     KH_CASE(KH_EPI_STORE16)
     KH_CASE(KH_EPI_F32)
@@ -347,7 +427,12 @@ int gemm(hipStream_t st, int epi, const void* A, int a_dtype, const kh_weight& W
   if (lda < K || lda % 8) return e.fail("gemm: lda=%d must be >= K and a multiple of 8", lda);
   if (ldw < N) return e.fail("gemm: ldw=%d < N=%d", ldw, N);
   const int out_cols = epi == KH_EPI_SWIGLU ? N / 2 : N;
-  if (ldc < out_cols || ldc % 4) return e.fail("gemm: ldc=%d must be >= %d and a multiple of 4", ldc, out_cols);
+  const bool out16 = epi == KH_EPI_STORE16 || epi == KH_EPI_GELU || epi == KH_EPI_BIAS16 || epi == KH_EPI_SWIGLU;
+  const int ldc_mult = out16 ? 8 : 4;  // output rows are written in 16-byte vectors
+  if (ldc < out_cols || ldc % ldc_mult)
+    return e.fail("gemm: ldc=%d must be >= %d and a multiple of %d", ldc, out_cols, ldc_mult);
+  if (((uintptr_t)C & 15) || ((uintptr_t)A & 15) || ((uintptr_t)W.w & 15))
+    return e.fail("gemm: A, W and C must be 16-byte aligned");
   const bool needs_vec = epi == KH_EPI_RESID_GATE || epi == KH_EPI_BIAS16 || epi == KH_EPI_BIAS_F32;
   if (needs_vec && !vec) return e.fail("gemm: epilogue %d needs vec", epi);
   int wf;
