@@ -1,0 +1,84 @@
+"""CPU checks of the drop-in boundary: libkh.so loads, exports every entry point include/kh.h declares, and
+rejects unsupported arguments with KH_EINVAL and a message before any HIP call (no GPU needed)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADERS = [os.path.join(ROOT, "include", f) for f in os.listdir(os.path.join(ROOT, "include")) if f.endswith(".h")]
+
+
+def declared_symbols():
+    names = set()
+    for h in HEADERS:
+        text = open(h).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"^[A-Za-z_][\w \*]*?\b(kh_\w+)\s*\(", text, flags=re.M):
+            names.add(m.group(1))
+    return sorted(names)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from krea_image_amd import kh
+    return kh.load()
+
+
+def test_header_declares_entry_points():
+    syms = declared_symbols()
+    assert "kh_gemm" in syms and "kh_version" in syms, syms
+
+
+def test_library_exports_every_declared_symbol(lib):
+    missing = [s for s in declared_symbols() if not hasattr(lib, s)]
+    assert not missing, f"declared in include/*.h but not exported by libkh.so: {missing}"
+
+
+def test_binding_symbol_list_matches_header():
+    from krea_image_amd import kh
+    assert sorted(kh.SYMBOLS) == declared_symbols()
+
+
+def test_version(lib):
+    assert b"gfx950" in lib.kh_version()
+
+
+def _gemm_call(lib, **kw):
+    from krea_image_amd import kh
+    args = dict(epi=0, A=16, a_dtype=kh.F16, M=64, N=64, K=64, lda=64, ldw=64, ldc=64, vec=None,
+                w=kh._WeightC(16, 16, kh.I8, kh.F16, 0))
+    args.update(kw)
+    err = ctypes.create_string_buffer(256)
+    w = args["w"]
+    rc = lib.kh_gemm(None, args["epi"], ctypes.c_void_p(args["A"]), args["a_dtype"],
+                     None if w is None else ctypes.byref(w), ctypes.c_void_p(16), args["M"], args["N"], args["K"],
+                     args["lda"], args["ldw"], args["ldc"], args["vec"], err, 256)
+    return rc, err.value.decode()
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(N=96), "N % 64"),
+    (dict(K=100, lda=100), "K % 64"),
+    (dict(M=0), "empty shape"),
+    (dict(epi=9), "unknown epilogue"),
+    (dict(a_dtype=0), "f16 or bf16"),
+    (dict(lda=32), "lda"),
+    (dict(ldc=60), "ldc"),
+    (dict(epi=2), "needs vec"),
+    (dict(w=None), "null weight"),
+    (dict(A=0), "null"),
+])
+def test_gemm_rejects_without_launch(lib, kw, msg):
+    rc, err = _gemm_call(lib, **kw)
+    assert rc == -1, (rc, err)
+    assert msg in err, err
+
+
+def test_gemm_rejects_bad_int8_group(lib):
+    from krea_image_amd import kh
+    rc, err = _gemm_call(lib, K=256, lda=256, w=kh._WeightC(16, 16, kh.I8, kh.F32, 96))
+    assert rc == -1 and "group" in err
+    rc, err = _gemm_call(lib, w=kh._WeightC(16, 16, kh.BF16, kh.F32, 0))
+    assert rc == -1 and "match the activation type" in err

@@ -114,3 +114,41 @@ def test_gemm_rejects_bad_shapes(dev):
     C = torch.zeros(64, 64, dtype=torch.float16, device=dev)
     with pytest.raises(kh.KhError, match="K % 64"):
         kh.gemm("store16", A, W, C, 64, 64, 96, 96, 64, 64)
+
+
+@pytest.mark.parametrize("epi", EPIS)
+def test_gemm_golden_fixture_per_channel(dev, epi):
+    """The kernels against tests/golden/gemm_ch.npz (numpy float64, independent of the oracle)."""
+    import os
+    from krea_image_amd import kh
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "gemm_ch.npz"), allow_pickle=False)
+    M, K = g["A"].shape
+    N = g["q"].shape[1]
+    ncol = N // 2 if epi == "swiglu" else N
+    Ad = to_dev16(g["A"], O.F16, dev)
+    W = kh.Weight(torch.from_numpy(g["q"]).to(dev), to_dev16(g["s"], O.F16, dev), K)
+    vec = torch.from_numpy(g["vec"]).to(dev)
+    if epi in F32_OUT:
+        C = torch.from_numpy(g["X0"].copy() if epi in ("resid", "resid_gate") else np.zeros((M, N), np.float32)).to(dev)
+    else:
+        C = torch.zeros(M, ncol, dtype=torch.float16, device=dev)
+    kh.gemm(epi, Ad, W, C, M, N, K, K, N, ncol, vec)
+    torch.cuda.synchronize()
+    got = C.cpu().numpy() if epi in F32_OUT else C.cpu().float().numpy()
+    ref = g["out_" + epi]
+    if epi in ("resid", "resid_gate"):
+        got, ref = got - g["X0"], ref - g["X0"]
+    assert rel_l2(got, ref) < (1e-3 if epi not in F32_OUT else 1e-5), epi
+
+
+def test_gemm_golden_fixture_group128_bf16(dev):
+    import os
+    from krea_image_amd import kh
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "gemm_g128.npz"), allow_pickle=False)
+    M, K = g["A"].shape
+    N = g["q"].shape[1]
+    C = torch.zeros(M, N, dtype=torch.bfloat16, device=dev)
+    kh.gemm("store16", to_dev16(g["A"], O.BF16, dev), kh.Weight(torch.from_numpy(g["q"]).to(dev),
+            torch.from_numpy(g["s"]).to(dev), 128), C, M, N, K, K, N, N)
+    torch.cuda.synchronize()
+    assert rel_l2(C.cpu().float().numpy(), g["out_store16"]) < 8e-3
