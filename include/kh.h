@@ -65,6 +65,16 @@ typedef struct kh_weight {
 int kh_gemm(kh_stream stream, int epi, const void* A, int a_dtype, const kh_weight* W, void* C, int M, int N, int K,
             int lda, int ldw, int ldc, const void* vec, char* err, int errlen);
 
+/* Flash attention, head dim 128: O[q, h] = softmax_k(Q[q,h] . K[k, h/group] / sqrt(128) (+ QB[q,h] KB[k,h/group]))
+ * V[k, h/group] (* sigmoid(G[q, h]) if G), fp32 scores / softmax / accumulation, P rounded to the 16-bit type
+ * before P V. Q [Lq, ldq], K [Lk, ldk], V [Lk, ldv], O [Lq, ldo], G [Lq, ldg] (dtype KH_F16 / KH_BF16), head h at
+ * column 128 h (kv head at 128 (h / group)). causal: key k visible to query i iff k <= i + q_pos0. QB [Lq, heads]
+ * and KB [Lk, heads / group] (f32, both or neither): the rank-1 score term of a "big" head dimension.
+ * Replaces krea::Metal::attention (engine/src/metal.h:86-88, engine/src/metal.mm:193-202). */
+int kh_attention(kh_stream stream, const void* Q, const void* K, const void* V, void* O, int dtype, int Lq, int Lk,
+                 int heads, int ldq, int ldk, int ldv, int ldo, int group, int causal, int q_pos0, const void* G,
+                 int ldg, const float* QB, const float* KB, char* err, int errlen);
+
 /* Library identification (for the loader checks of the host bindings). */
 const char* kh_version(void);
 

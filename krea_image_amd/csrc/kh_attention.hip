@@ -1,0 +1,292 @@
+// Flash attention forward for MI355X (gfx950), head dim 128, fp16 / bf16 in and out, fp32 scores, softmax
+// and accumulation: the joint image + text attention of the Krea 2 DiT.
+//
+// Semantics: engine/kernels/attention.metal:131-351 (attention_d128) as dispatched by
+// engine/src/metal.mm:193-202 (Metal::attention):
+//   O[q, h] = softmax_k(Q[q, h] . K[k, h / group] / sqrt(128) (+ QB[q, h] KB[k, h / group])) V[k, h / group]
+//             (* sigmoid(G[q, h]) when a gate is given), optional causal mask key <= q + q_pos0.
+// P is rounded to the 16-bit type before P V (attention.metal:272-276); row sums use the unrounded p.
+//
+// Design (CDNA4, v_mfma_f32_32x32x16):
+//  * Transposed products: S^T = K Q^T (K is the A operand straight from LDS, Q^T the B operand held in
+//    registers for the whole key loop) and O^T += V^T P^T. In the 32 x 32 accumulator layout a lane owns
+//    one query column, so the running max / sum and the O rescale are per-lane scalars: no row shuffles
+//    except one lane-pair exchange (lane l, l ^ 32) per key block.
+//  * P^T is fed to the second MFMA straight from the S^T registers: within a 16-key step the lane's keys are
+//    {4h .. 4h+3, 8+4h .. 8+4h+3} (h = lane / 32), and the V^T operand is read in that same key order, so
+//    the contraction needs no data movement (the key order inside a step is irrelevant to the sum).
+//  * K tiles stream global -> LDS directly (16-byte DMA per lane), rows of 256 B with the 16-byte chunk
+//    XOR-swizzled by (row & 15). V tiles are transposed on the way in (4 keys x 8 dims per thread,
+//    v_perm_b32 into 8 dims x 4 keys) into V^T rows of 128 B, chunk XOR (d & 7) ^ (d >> 3 & 7).
+//  * 4 waves x 32 queries per workgroup, 64-key blocks double-buffered (2 x 32 KB); two workgroups per CU.
+//  * Lazy online softmax (the reference's LAZY_TH idea, attention.metal:33-37): the running max only moves
+//    when a block's max exceeds it by more than 8 (log2 units), so most blocks skip the O rescale.
+#include "kh_common.h"
+#include "kh_internal.h"
+
+namespace kh {
+
+namespace {
+
+constexpr int D = 128, BQ = 128, BKEYS = 64, NTHR = 256;
+constexpr int KT_BYTES = BKEYS * D * 2;   // K tile: 64 rows x 256 B
+constexpr int VT_BYTES = D * BKEYS * 2;   // V^T tile: 128 rows x 128 B
+constexpr int BUF = KT_BYTES + VT_BYTES;  // one pipeline stage
+constexpr float LAZY_TH = 8.0f;
+constexpr float M_INIT = -1.0e30f;        // finite: a fully masked block leaves exp2(-inf - M_INIT) = 0
+
+struct AttnArgs {
+  const void *Q, *K, *V;
+  void* O;
+  const void* G;
+  const float *QB, *KB;
+  int Lq, Lk, heads, ldq, ldk, ldv, ldo, group, q_pos0, ldg, ldqb, ldkb;
+  float scale_log2;
+};
+
+template <int DT>
+__device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, const f32x16& c) {
+  if constexpr (DT == KH_BF16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                   0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                                  0);
+}
+
+__device__ __forceinline__ int vt_chunk(int d, int kc) { return kc ^ (d & 7) ^ ((d >> 3) & 7); }
+
+template <int DT, bool GATE, bool BIG, bool CAUSAL>
+__global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
+  __shared__ __attribute__((aligned(1024))) char lds[2 * BUF];
+  __shared__ float kb_s[2][BKEYS];  // fp32 rank-1 key term of the staged block (BIG)
+  typedef __attribute__((address_space(3))) void lds_void;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hh = lane >> 5;
+  const int h = blockIdx.y, kvh = h / p.group;
+  const int qblk = blockIdx.x * BQ;
+  const int q = qblk + wave * 32 + l32;       // this lane's query
+  const int qc = min(q, p.Lq - 1);            // clamped (rows >= Lq are computed, never stored)
+
+  // ---- Q^T fragments (B operand): d-step s covers d [16 s, 16 s + 16); lane half hh holds 8 of them ----
+  u32x4 qf[8];
+  {
+    const uint16_t* qp = (const uint16_t*)p.Q + (size_t)qc * p.ldq + h * D + hh * 8;
+#pragma unroll
+    for (int s = 0; s < 8; s++) qf[s] = *(const u32x4*)(qp + s * 16);
+  }
+  const float qb = BIG ? p.QB[(size_t)qc * p.ldqb + h] : 0.f;
+
+  // key range of this workgroup (causal: up to its last query's visible key)
+  int kend = p.Lk;
+  if (CAUSAL) kend = max(0, min(p.Lk, qblk + BQ + p.q_pos0));
+  const int nblk = (kend + BKEYS - 1) / BKEYS;
+
+  // ---- K tile DMA: instruction r of wave w fills 1 KB = rows 4 (4 r + w) .. +3; lane -> row lane / 16,
+  //      chunk slot lane & 15 receives logical chunk (lane & 15) ^ (row & 15) ----
+  const uint16_t* kbase = (const uint16_t*)p.K + kvh * D;
+  auto issue_k = [&](int b, int buf) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int row = 4 * (4 * r + wave) + (lane >> 4);
+      const int key = min(b * BKEYS + row, p.Lk - 1);
+      const int c = (lane & 15) ^ (row & 15);
+      __builtin_amdgcn_global_load_lds((const void*)(kbase + (size_t)key * p.ldk + c * 8),
+                                       (lds_void*)(lds + buf * BUF + (4 * r + wave) * 1024), 16, 0, 0);
+    }
+  };
+  // ---- V tile: thread -> keys 4 kq .. 4 kq + 3 (kq = tid / 16), dims 8 c .. 8 c + 7 (c = tid & 15) ----
+  const int vkq = tid >> 4, vc = tid & 15;
+  const uint16_t* vbase = (const uint16_t*)p.V + kvh * D + vc * 8;
+  u32x4 vr[4];
+  auto load_v = [&](int b) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int key = min(b * BKEYS + 4 * vkq + r, p.Lk - 1);
+      vr[r] = *(const u32x4*)(vbase + (size_t)key * p.ldv);
+    }
+  };
+  auto store_vt = [&](int buf) {  // 8 dims x 4 keys: V^T[d][4 kq .. 4 kq + 3] as one 8-byte write per d
+    char* vt = lds + buf * BUF + KT_BYTES;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int d = vc * 8 + i;
+      const int w = i >> 1;  // dword of the 16-byte row chunk holding dims 2w, 2w + 1
+      const uint32_t sel = (i & 1) ? 0x07060302u : 0x05040100u;
+      const uint32_t lo = __builtin_amdgcn_perm(vr[1][w], vr[0][w], sel);  // keys 4kq, 4kq+1 of dim d
+      const uint32_t hi = __builtin_amdgcn_perm(vr[3][w], vr[2][w], sel);  // keys 4kq+2, 4kq+3
+      const int kc = vkq >> 1;  // 16-byte chunk (8 keys) of the V^T row
+      *(u32x2*)(vt + d * 128 + vt_chunk(d, kc) * 16 + (vkq & 1) * 8) = (u32x2){lo, hi};
+    }
+  };
+  auto stage_kb = [&](int b, int buf) {
+    if (BIG && tid < BKEYS) kb_s[buf][tid] = p.KB[(size_t)min(b * BKEYS + tid, p.Lk - 1) * p.ldkb + kvh];
+  };
+
+  f32x16 o[4];
+#pragma unroll
+  for (int db = 0; db < 4; db++) o[db] = (f32x16){};
+  float m = M_INIT, l = 0.f;
+
+  if (nblk > 0) {
+    issue_k(0, 0);
+    load_v(0);
+    stage_kb(0, 0);
+    store_vt(0);
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
+    lds_barrier();
+  }
+  for (int b = 0; b < nblk; b++) {
+    const int cur = b & 1;
+    const bool has_next = b + 1 < nblk;
+    if (has_next) {
+      issue_k(b + 1, cur ^ 1);
+      load_v(b + 1);
+      stage_kb(b + 1, cur ^ 1);
+    }
+    const char* kt = lds + cur * BUF;
+    const char* vt = kt + KT_BYTES;
+
+    // S^T = K Q^T: st[kh] holds keys 32 kh + 8 (i / 4) + 4 hh + i % 4 (i = 0..15) of query q
+    f32x16 st[2];
+#pragma unroll
+    for (int kh = 0; kh < 2; kh++) {
+      st[kh] = (f32x16){};
+      const int krow = kh * 32 + l32;
+#pragma unroll
+      for (int s = 0; s < 8; s++) {
+        const u32x4 kf = *(const u32x4*)(kt + krow * 256 + (((2 * s + hh) ^ (krow & 15)) * 16));
+        st[kh] = mfma32<DT>(kf, qf[s], st[kh]);
+      }
+    }
+
+    // scores in log2 units, masking, block max
+    const int key0 = b * BKEYS;
+    const bool need_mask = CAUSAL || (key0 + BKEYS > p.Lk);
+    float bmax = -INFINITY;
+#pragma unroll
+    for (int kh = 0; kh < 2; kh++)
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const int kl = kh * 32 + (i >> 2) * 8 + hh * 4 + (i & 3);
+        float s = st[kh][i];
+        if (BIG) s += qb * kb_s[cur][kl];
+        s *= p.scale_log2;
+        if (need_mask) {
+          const int key = key0 + kl;
+          if (key >= p.Lk || (CAUSAL && key > q + p.q_pos0)) s = -INFINITY;
+        }
+        st[kh][i] = s;
+        bmax = fmaxf(bmax, s);
+      }
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+    // lazy max update: only when some query of the wave grew by more than LAZY_TH
+    const bool grow = bmax > m + LAZY_TH;
+    if (__any(grow)) {
+      const float m_new = fmaxf(m, bmax);
+      const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+      m = m_new;
+      l *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; db++) o[db] *= alpha;
+    }
+
+    // P^T = exp2(s - m) as the 16-bit B operand of O^T += V^T P^T; key step j uses st[j / 2][8 (j & 1) ..]
+    u32x4 pf[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const float p0 = __builtin_amdgcn_exp2f(st[j >> 1][(j & 1) * 8 + 2 * e] - m);
+        const float p1 = __builtin_amdgcn_exp2f(st[j >> 1][(j & 1) * 8 + 2 * e + 1] - m);
+        l += p0 + p1;
+        pf[j][e] = (uint32_t)to16<DT>(p0) | ((uint32_t)to16<DT>(p1) << 16);
+      }
+    }
+#pragma unroll
+    for (int db = 0; db < 4; db++) {
+      const int d = db * 32 + l32;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int k0 = 16 * j + 4 * hh, k1 = k0 + 8;  // keys of operand slots 0..3 and 4..7
+        const u32x2 a = *(const u32x2*)(vt + d * 128 + vt_chunk(d, k0 >> 3) * 16 + (k0 & 7) * 2);
+        const u32x2 c = *(const u32x2*)(vt + d * 128 + vt_chunk(d, k1 >> 3) * 16 + (k1 & 7) * 2);
+        o[db] = mfma32<DT>((u32x4){a[0], a[1], c[0], c[1]}, pf[j], o[db]);
+      }
+    }
+
+    if (has_next) {
+      store_vt(cur ^ 1);
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));  // vmcnt(0): the next K tile has landed
+    }
+    lds_barrier();
+  }
+
+  // ---- normalise, gate, store: lane holds d = 32 db + 8 g + 4 hh + e of query q ----
+  l += __shfl_xor(l, 32);
+  if (q >= p.Lq) return;
+  const float inv = l > 0.f ? 1.0f / l : 0.f;
+  uint16_t* op = (uint16_t*)p.O + (size_t)q * p.ldo + h * D;
+  const uint16_t* gp = GATE ? (const uint16_t*)p.G + (size_t)q * p.ldg + h * D : nullptr;
+#pragma unroll
+  for (int db = 0; db < 4; db++)
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      const int d = db * 32 + g * 8 + hh * 4;
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) v[e] = o[db][g * 4 + e] * inv;
+      if (GATE) {
+        const u32x2 gv = *(const u32x2*)(gp + d);
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[e] *= sigmoid_fast(from16<DT>((uint16_t)(gv[e >> 1] >> (16 * (e & 1)))));
+      }
+      *(u32x2*)(op + d) = (u32x2){(uint32_t)to16<DT>(v[0]) | ((uint32_t)to16<DT>(v[1]) << 16),
+                                  (uint32_t)to16<DT>(v[2]) | ((uint32_t)to16<DT>(v[3]) << 16)};
+    }
+}
+
+template <int DT, bool GATE, bool BIG>
+hipError_t launch3(bool causal, const AttnArgs& a, hipStream_t st) {
+  dim3 grid((a.Lq + BQ - 1) / BQ, a.heads), block(NTHR);
+  if (causal)
+    hipLaunchKernelGGL((attn_kernel<DT, GATE, BIG, true>), grid, block, 0, st, a);
+  else
+    hipLaunchKernelGGL((attn_kernel<DT, GATE, BIG, false>), grid, block, 0, st, a);
+  return hipGetLastError();
+}
+
+template <int DT>
+hipError_t launch2(bool gate, bool big, bool causal, const AttnArgs& a, hipStream_t st) {
+  if (gate) return big ? launch3<DT, true, true>(causal, a, st) : launch3<DT, true, false>(causal, a, st);
+  return big ? launch3<DT, false, true>(causal, a, st) : launch3<DT, false, false>(causal, a, st);
+}
+
+}  // namespace
+
+int attention(hipStream_t st, const void* Q, const void* K, const void* V, void* O, int dtype, int Lq, int Lk,
+              int heads, int ldq, int ldk, int ldv, int ldo, int group, int causal, int q_pos0, const void* G,
+              int ldg, const float* QB, const float* KB, Err& e) {
+  if (dtype != KH_F16 && dtype != KH_BF16) return e.fail("attention: dtype must be f16 or bf16");
+  if (Lq <= 0 || Lk <= 0 || heads <= 0) return e.fail("attention: empty shape Lq=%d Lk=%d heads=%d", Lq, Lk, heads);
+  if (group <= 0 || heads % group) return e.fail("attention: heads %d not a multiple of group %d", heads, group);
+  if (!Q || !K || !V || !O) return e.fail("attention: null Q / K / V / O");
+  const int kv_heads = heads / group;
+  if (ldq < heads * D || ldo < heads * D || ldk < kv_heads * D || ldv < kv_heads * D)
+    return e.fail("attention: row strides too small for %d heads of 128", heads);
+  if (ldq % 8 || ldk % 8 || ldv % 8 || ldo % 4) return e.fail("attention: strides must keep 16-byte rows");
+  if (((uintptr_t)Q | (uintptr_t)K | (uintptr_t)V) & 15) return e.fail("attention: Q, K, V must be 16-byte aligned");
+  if (((uintptr_t)O & 7)) return e.fail("attention: O must be 8-byte aligned");
+  if (G && (ldg < heads * D || ldg % 4 || ((uintptr_t)G & 7))) return e.fail("attention: bad gate stride / alignment");
+  if ((QB == nullptr) != (KB == nullptr)) return e.fail("attention: QB and KB go together");
+  if (Lq > (1 << 24) / 1 || (size_t)Lk * ldk > ((size_t)1 << 31)) return e.fail("attention: too large");
+  AttnArgs a{Q, K, V, O, G, QB, KB, Lq, Lk, heads, ldq, ldk, ldv, ldo, group, q_pos0, ldg, heads, kv_heads,
+             (float)(1.4426950408889634 / 11.313708498984761)};
+  const hipError_t r = dtype == KH_F16 ? launch2<KH_F16>(G != nullptr, QB != nullptr, causal != 0, a, st)
+                                       : launch2<KH_BF16>(G != nullptr, QB != nullptr, causal != 0, a, st);
+  if (r != hipSuccess) return e.hip(r, "attention launch");
+  return KH_OK;
+}
+
+}  // namespace kh

@@ -58,5 +58,15 @@ __device__ __forceinline__ float gelu_fast(float x) {
   return x * rcp_fast(1.0f + __expf(-2.0f * u));
 }
 __device__ __forceinline__ float silu_fast(float x) { return x * rcp_fast(1.0f + __expf(-x)); }
+__device__ __forceinline__ float sigmoid_fast(float x) { return rcp_fast(1.0f + __expf(-x)); }
+
+// s_waitcnt immediate (gfx9 encoding): vmcnt <= vm, lgkmcnt <= lgkm, expcnt untouched.
+__host__ __device__ constexpr int waitcnt_imm(int vm, int lgkm) {
+  return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | (lgkm << 8);
+}
+
+// Workgroup barrier that is also a compiler memory barrier, without the release fence of __syncthreads
+// (which would also wait for LDS-direct loads still streaming in for later pipeline stages).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 }  // namespace kh

@@ -60,15 +60,6 @@ struct GemmArgs {
 // {j, j+4, ..., j+28} (the weight writes: lane L writes row 4L + j).
 __device__ __forceinline__ int swz(int row) { return (row ^ (row >> 2)) & 7; }
 
-// s_waitcnt immediate (gfx9 encoding): vmcnt <= vm, lgkmcnt <= lgkm, expcnt untouched.
-__host__ __device__ constexpr int waitcnt_imm(int vm, int lgkm) {
-  return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | (lgkm << 8);
-}
-
-// Workgroup barrier that is also a compiler memory barrier, without the release fence of __syncthreads
-// (which would wait for the activation tiles still streaming into LDS for later K steps).
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
 template <int ACT>
 __device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, const f32x16& c) {
   if constexpr (ACT == KH_BF16)

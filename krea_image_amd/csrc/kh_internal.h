@@ -35,4 +35,8 @@ struct Err {
 int gemm(hipStream_t st, int epi, const void* A, int a_dtype, const kh_weight& W, void* C, int M, int N, int K,
          int lda, int ldw, int ldc, const void* vec, Err& e);
 
+int attention(hipStream_t st, const void* Q, const void* K, const void* V, void* O, int dtype, int Lq, int Lk,
+              int heads, int ldq, int ldk, int ldv, int ldo, int group, int causal, int q_pos0, const void* G,
+              int ldg, const float* QB, const float* KB, Err& e);
+
 }  // namespace kh

@@ -27,7 +27,7 @@ Epi = type("Epi", (), {"BF16": 0, "STORE16": 0, "F32": 1, "ResidGate": 2, "Resid
 _TORCH_DT = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16, torch.int8: I8}
 
 # C-ABI symbols declared in include/kh.h (checked by tests/test_abi.py)
-SYMBOLS = ["kh_version", "kh_gemm"]
+SYMBOLS = ["kh_version", "kh_gemm", "kh_attention"]
 
 
 class KhError(RuntimeError):
@@ -53,6 +53,9 @@ def load():
         vp, i = ctypes.c_void_p, ctypes.c_int
         lib.kh_gemm.argtypes = [vp, i, vp, i, ctypes.POINTER(_WeightC), vp, i, i, i, i, i, i, vp, ctypes.c_char_p, i]
         lib.kh_gemm.restype = i
+        lib.kh_attention.argtypes = [vp, vp, vp, vp, vp, i, i, i, i, i, i, i, i, i, i, i, vp, i, vp, vp,
+                                     ctypes.c_char_p, i]
+        lib.kh_attention.restype = i
         _lib = lib
     return _lib
 
@@ -117,3 +120,17 @@ def linear(epi, x: torch.Tensor, W: Weight, out: Optional[torch.Tensor] = None, 
         dt = torch.float32 if epi in (EPI["f32"], EPI["bias_f32"]) else x.dtype
         out = torch.empty(M, N // 2 if epi == EPI["swiglu"] else N, dtype=dt, device=x.device)
     return gemm(epi, x, W, out, M, N, K, x.stride(0), W.w.stride(0), out.stride(0), vec)
+
+
+def attention(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, O: torch.Tensor, Lq: int, Lk: int, heads: int,
+              ldq: int, ldk: int, ldv: int, ldo: int, group: int = 1, causal: bool = False, q_pos0: int = 0,
+              G: Optional[torch.Tensor] = None, ldg: int = 0, QB: Optional[torch.Tensor] = None,
+              KB: Optional[torch.Tensor] = None):
+    """krea::Metal::attention (engine/src/metal.mm:193-202): flash attention, head dim 128. Tensors may be
+    column views of a fused projection buffer (their data_ptr is the first element of head 0)."""
+    lib = load()
+    err = ctypes.create_string_buffer(512)
+    rc = lib.kh_attention(_stream(), _ptr(Q), _ptr(K), _ptr(V), _ptr(O), dtype_code(Q.dtype), Lq, Lk, heads, ldq, ldk,
+                          ldv, ldo, group, int(causal), q_pos0, _ptr(G), ldg, _ptr(QB), _ptr(KB), err, 512)
+    _check(rc, err)
+    return O
