@@ -75,6 +75,97 @@ int kh_attention(kh_stream stream, const void* Q, const void* K, const void* V, 
                  int heads, int ldq, int ldk, int ldv, int ldo, int group, int causal, int q_pos0, const void* G,
                  int ldg, const float* QB, const float* KB, char* err, int errlen);
 
+/* Row norm with modulation: y = (x - mu) * rsqrt(mean((x - mu)^2) + eps) * mul (+ add), mu = 0 (center = 0,
+ * RMSNorm as in the reference) or the row mean (center = 1, LayerNorm of the benchmark configs); x f32
+ * [rows, ld_in], width % 4 == 0, width <= 8192, y in out_dtype (KH_F32 / KH_F16 / KH_BF16).
+ * Replaces krea::Metal::rms_norm (engine/src/metal.h:72-74, engine/kernels/norm.metal:28-55). */
+int kh_rms_norm(kh_stream stream, const float* x, const float* mul, const float* add, void* y, int out_dtype, int rows,
+                int width, int ld_in, int ld_out, float eps, int center, char* err, int errlen);
+
+/* Per-head RMSNorm (f32 weights [128]) + RoPE in place on a 16-bit fused projection buffer [rows, ld]: n_q heads
+ * at column q_off, n_k heads at k_off. rope_mode 0: interleaved pairs (2i, 2i+1), 1: rotate-half (i, i+64),
+ * 2: none; cos / sin f32 [rows, 64]. big_dim >= 0: that dimension goes to qbig [rows, n_q] / kbig [rows, n_k]
+ * (f32) and is zeroed. Replaces krea::Metal::qk_norm_rope (engine/src/metal.h:77-79, norm.metal:81-134). */
+int kh_qk_norm_rope(kh_stream stream, void* qkv, int dtype, const float* wq, const float* wk, const float* cosb,
+                    const float* sinb, int rows, int ld, int q_off, int n_q, int k_off, int n_k, float eps,
+                    int rope_mode, int big_dim, float* qbig, float* kbig, char* err, int errlen);
+
+/* adaLN modulation GEMV: y[r, n] = (y[r, n] if act & 2) + sum_k act1(x[r, k]) W~[k, n] + bias[n] (bias may be
+ * NULL), act & 1 = SiLU on load; rows 1..4, x [rows, K] / y [rows, N] f32, W as in kh_gemm (int8 per-channel or
+ * group, or 16-bit). Column sums are combined with f32 atomics (summation order not fixed).
+ * Replaces the gemv_bf16 kernel (engine/kernels/gemm.metal:346-371) and the CPU cblas_sgemv of
+ * Conditioning::compute (engine/src/model.mm:571-591). */
+int kh_gemv(kh_stream stream, const float* x, const kh_weight* W, float* y, int rows, int N, int K, int ldw, int act,
+            const float* bias, char* err, int errlen);
+
+/* Modulation vectors of one layer from the adaLN output: engine/src/model.mm:317-347 (DiT::make_cond), on the
+ * device. tvec [6 D], table [6 D] or NULL, n1 / n2 [D] -> mods [6 D] = [n1 (1+v0), v1, v2, n2 (1+v3), v4, v5]. */
+int kh_make_cond(kh_stream stream, const float* tvec, const float* table, const float* n1, const float* n2, int D,
+                 float* mods, char* err, int errlen);
+
+/* fp32 GEMM (patch embed / final projection): C = A[M,K] x W[K,N] with mode bit 0 + bias[N], bit 1 GELU(tanh),
+ * bit 2 accumulate into C. Replaces krea::Metal::gemm_f32 (engine/src/metal.h:70-71, f32gemm.metal). */
+int kh_gemm_f32(kh_stream stream, const float* A, const float* W, float* C, int M, int N, int K, int lda, int ldw,
+                int ldc, int mode, const float* bias, char* err, int errlen);
+
+/* RoPE tables on the HOST: cos / sin [T + H*W, 64] f32 for T text rows at the origin and an H x W image grid.
+ * mode 0: the reference's 3 axes (theta 1000, pairs 16 / 24 / 24; DiT::set_grid, engine/src/model.mm:290-315);
+ * mode 1: 2-D, theta 10000, pairs [0, 32) by row and [32, 64) by column (benchmark configs). */
+int kh_rope_tables(int T, int H, int W, int mode, float* cosb, float* sinb);
+
+/* ---- one DiT block on the device: engine/src/model.mm:369-385 (DiT::layer) ---- */
+typedef struct kh_dit_config {
+  int dim;         /* hidden size D */
+  int heads;       /* query heads of 128 */
+  int kv_heads;    /* key / value heads (GQA: heads % kv_heads == 0) */
+  int ff;          /* MLP hidden units */
+  int mlp;         /* 0: GELU(tanh) MLP (up N = ff); 1: SwiGLU (up N = 2 ff, gate|up 64-column tile interleave) */
+  int attn_gate;   /* 1: the q|k|v projection also carries a gate block [D]; attention output *= sigmoid(gate) */
+  int norm_center; /* 0: RMSNorm pre-norms (reference); 1: LayerNorm pre-norms */
+  int rope_mode;   /* kh_qk_norm_rope mode */
+  int dtype;       /* activation type KH_F16 / KH_BF16 */
+  float eps;       /* norm epsilon (pre-norms and QK norms) */
+} kh_dit_config;
+
+typedef struct kh_dit_layer {
+  kh_weight qkv;          /* [D, D + 2 kv_heads 128 (+ D gate)]: q | k | v (| gate), convert.py:189-224 layout */
+  kh_weight o;            /* [D, D] */
+  kh_weight up;           /* [D, ff] (GELU) or [D, 2 ff] interleaved (SwiGLU) */
+  kh_weight down;         /* [ff, D] */
+  kh_weight ada;          /* adaLN linear [cond_dim, 6 D]; ada.w == NULL: the caller fills state->mods */
+  const float* ada_bias;  /* [6 D] or NULL */
+  const float* mod_table; /* [6 D] per-layer table added to the adaLN output, or NULL */
+  const float* n1;        /* [D] pre-attention norm weight (stored as 1 + w) */
+  const float* n2;        /* [D] pre-MLP norm weight */
+  const float* qn;        /* [128] q norm weight */
+  const float* kn;        /* [128] k norm weight */
+  int big_dim;            /* head dimension carried in fp32 (QB / KB), or -1 */
+} kh_dit_layer;
+
+typedef struct kh_dit_state { /* device buffers, owned by the caller; rows R = text + image tokens */
+  float* x;           /* [R, D] f32 residual stream */
+  void* h;            /* [R, D] normalised activations */
+  void* qkv;          /* [R, D + 2 kvD (+ D)] */
+  void* ao;           /* [R, D] attention output */
+  void* mid;          /* [R, ff] MLP hidden */
+  float* tvec;        /* [6 D] adaLN output */
+  float* mods;        /* [6 D] modulation vectors */
+  const float* cond;  /* [cond_dim] conditioning embedding (SiLU applied by the adaLN GEMV) */
+  int cond_dim;
+  const float* cosb;  /* [R, 64] RoPE tables */
+  const float* sinb;
+  float* qbig;        /* [R, heads] (layers with big_dim >= 0) */
+  float* kbig;        /* [R, kv_heads] */
+} kh_dit_state;
+
+/* One layer: adaLN (GEMV + make_cond) -> norm -> qkv GEMM -> QK norm + RoPE -> attention -> O GEMM with gated
+ * residual -> norm -> MLP up (GELU / SwiGLU) -> down GEMM with gated residual. Asynchronous on `stream`. */
+int kh_dit_layer_forward(kh_stream stream, const kh_dit_config* cfg, const kh_dit_layer* layer,
+                         const kh_dit_state* state, int rows, char* err, int errlen);
+/* Layers [0, n_layers) in order (engine/src/model.mm:519-525, DiT::run_layers). */
+int kh_dit_forward(kh_stream stream, const kh_dit_config* cfg, const kh_dit_layer* layers, int n_layers,
+                   const kh_dit_state* state, int rows, char* err, int errlen);
+
 /* Library identification (for the loader checks of the host bindings). */
 const char* kh_version(void);
 

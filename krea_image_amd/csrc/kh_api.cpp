@@ -22,4 +22,62 @@ int kh_attention(kh_stream stream, const void* Q, const void* K, const void* V, 
                        q_pos0, G, ldg, QB, KB, e);
 }
 
+int kh_rms_norm(kh_stream stream, const float* x, const float* mul, const float* add, void* y, int out_dtype, int rows,
+                int width, int ld_in, int ld_out, float eps, int center, char* err, int errlen) {
+  kh::Err e{err, errlen};
+  e.clear();
+  return kh::rms_norm((hipStream_t)stream, x, mul, add, y, out_dtype, rows, width, ld_in, ld_out, eps, center, e);
+}
+
+int kh_qk_norm_rope(kh_stream stream, void* qkv, int dtype, const float* wq, const float* wk, const float* cosb,
+                    const float* sinb, int rows, int ld, int q_off, int n_q, int k_off, int n_k, float eps,
+                    int rope_mode, int big_dim, float* qbig, float* kbig, char* err, int errlen) {
+  kh::Err e{err, errlen};
+  e.clear();
+  return kh::qk_norm_rope((hipStream_t)stream, qkv, dtype, wq, wk, cosb, sinb, rows, ld, q_off, n_q, k_off, n_k, eps,
+                          rope_mode, big_dim, qbig, kbig, e);
+}
+
+int kh_gemv(kh_stream stream, const float* x, const kh_weight* W, float* y, int rows, int N, int K, int ldw, int act,
+            const float* bias, char* err, int errlen) {
+  kh::Err e{err, errlen};
+  e.clear();
+  if (!W) return e.fail("gemv: null weight descriptor");
+  return kh::gemv((hipStream_t)stream, x, *W, y, rows, N, K, ldw, act, bias, e);
+}
+
+int kh_make_cond(kh_stream stream, const float* tvec, const float* table, const float* n1, const float* n2, int D,
+                 float* mods, char* err, int errlen) {
+  kh::Err e{err, errlen};
+  e.clear();
+  return kh::make_cond((hipStream_t)stream, tvec, table, n1, n2, D, mods, e);
+}
+
+int kh_gemm_f32(kh_stream stream, const float* A, const float* W, float* C, int M, int N, int K, int lda, int ldw,
+                int ldc, int mode, const float* bias, char* err, int errlen) {
+  kh::Err e{err, errlen};
+  e.clear();
+  return kh::gemm_f32((hipStream_t)stream, A, W, C, M, N, K, lda, ldw, ldc, mode, bias, e);
+}
+
+int kh_rope_tables(int T, int H, int W, int mode, float* cosb, float* sinb) {
+  return kh::rope_tables(T, H, W, mode, cosb, sinb);
+}
+
+int kh_dit_layer_forward(kh_stream stream, const kh_dit_config* cfg, const kh_dit_layer* layer,
+                         const kh_dit_state* state, int rows, char* err, int errlen) {
+  kh::Err e{err, errlen};
+  e.clear();
+  if (!cfg || !layer || !state) return e.fail("dit: null config / layer / state");
+  return kh::dit_layer_forward((hipStream_t)stream, *cfg, *layer, *state, rows, e);
+}
+
+int kh_dit_forward(kh_stream stream, const kh_dit_config* cfg, const kh_dit_layer* layers, int n_layers,
+                   const kh_dit_state* state, int rows, char* err, int errlen) {
+  kh::Err e{err, errlen};
+  e.clear();
+  if (!cfg || !state) return e.fail("dit: null config / state");
+  return kh::dit_forward((hipStream_t)stream, *cfg, layers, n_layers, *state, rows, e);
+}
+
 }  // extern "C"

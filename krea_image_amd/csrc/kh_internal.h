@@ -39,4 +39,21 @@ int attention(hipStream_t st, const void* Q, const void* K, const void* V, void*
               int heads, int ldq, int ldk, int ldv, int ldo, int group, int causal, int q_pos0, const void* G,
               int ldg, const float* QB, const float* KB, Err& e);
 
+int rms_norm(hipStream_t st, const float* x, const float* mul, const float* add, void* y, int out_dtype, int rows,
+             int width, int ld_in, int ld_out, float eps, int center, Err& e);
+int qk_norm_rope(hipStream_t st, void* qkv, int dtype, const float* wq, const float* wk, const float* cosb,
+                 const float* sinb, int rows, int ld, int q_off, int n_q, int k_off, int n_k, float eps, int rope_mode,
+                 int big_dim, float* qbig, float* kbig, Err& e);
+int gemv(hipStream_t st, const float* x, const kh_weight& W, float* y, int rows, int N, int K, int ldw, int act,
+         const float* bias, Err& e);
+int make_cond(hipStream_t st, const float* tvec, const float* table, const float* n1, const float* n2, int D,
+              float* mods, Err& e);
+int gemm_f32(hipStream_t st, const float* A, const float* W, float* C, int M, int N, int K, int lda, int ldw, int ldc,
+             int mode, const float* bias, Err& e);
+int dit_layer_forward(hipStream_t st, const kh_dit_config& c, const kh_dit_layer& L, const kh_dit_state& s, int R,
+                      Err& e);
+int dit_forward(hipStream_t st, const kh_dit_config& c, const kh_dit_layer* layers, int n, const kh_dit_state& s,
+                int R, Err& e);
+int rope_tables(int T, int H, int W, int mode, float* cosb, float* sinb);
+
 }  // namespace kh

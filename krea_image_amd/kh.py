@@ -27,7 +27,8 @@ Epi = type("Epi", (), {"BF16": 0, "STORE16": 0, "F32": 1, "ResidGate": 2, "Resid
 _TORCH_DT = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16, torch.int8: I8}
 
 # C-ABI symbols declared in include/kh.h (checked by tests/test_abi.py)
-SYMBOLS = ["kh_version", "kh_gemm", "kh_attention"]
+SYMBOLS = ["kh_version", "kh_gemm", "kh_attention", "kh_rms_norm", "kh_qk_norm_rope", "kh_gemv", "kh_make_cond",
+           "kh_gemm_f32", "kh_rope_tables", "kh_dit_layer_forward", "kh_dit_forward"]
 
 
 class KhError(RuntimeError):
@@ -37,6 +38,28 @@ class KhError(RuntimeError):
 class _WeightC(ctypes.Structure):
     _fields_ = [("w", ctypes.c_void_p), ("s", ctypes.c_void_p), ("w_dtype", ctypes.c_int),
                 ("s_dtype", ctypes.c_int), ("group", ctypes.c_int)]
+
+
+class DitConfig(ctypes.Structure):
+    """kh_dit_config (include/kh.h)."""
+    _fields_ = [("dim", ctypes.c_int), ("heads", ctypes.c_int), ("kv_heads", ctypes.c_int), ("ff", ctypes.c_int),
+                ("mlp", ctypes.c_int), ("attn_gate", ctypes.c_int), ("norm_center", ctypes.c_int),
+                ("rope_mode", ctypes.c_int), ("dtype", ctypes.c_int), ("eps", ctypes.c_float)]
+
+
+class DitLayerC(ctypes.Structure):
+    """kh_dit_layer (include/kh.h)."""
+    _fields_ = [("qkv", _WeightC), ("o", _WeightC), ("up", _WeightC), ("down", _WeightC), ("ada", _WeightC),
+                ("ada_bias", ctypes.c_void_p), ("mod_table", ctypes.c_void_p), ("n1", ctypes.c_void_p),
+                ("n2", ctypes.c_void_p), ("qn", ctypes.c_void_p), ("kn", ctypes.c_void_p), ("big_dim", ctypes.c_int)]
+
+
+class DitStateC(ctypes.Structure):
+    """kh_dit_state (include/kh.h)."""
+    _fields_ = [("x", ctypes.c_void_p), ("h", ctypes.c_void_p), ("qkv", ctypes.c_void_p), ("ao", ctypes.c_void_p),
+                ("mid", ctypes.c_void_p), ("tvec", ctypes.c_void_p), ("mods", ctypes.c_void_p),
+                ("cond", ctypes.c_void_p), ("cond_dim", ctypes.c_int), ("cosb", ctypes.c_void_p),
+                ("sinb", ctypes.c_void_p), ("qbig", ctypes.c_void_p), ("kbig", ctypes.c_void_p)]
 
 
 _lib = None
@@ -56,6 +79,20 @@ def load():
         lib.kh_attention.argtypes = [vp, vp, vp, vp, vp, i, i, i, i, i, i, i, i, i, i, i, vp, i, vp, vp,
                                      ctypes.c_char_p, i]
         lib.kh_attention.restype = i
+        f = ctypes.c_float
+        cp = ctypes.c_char_p
+        lib.kh_rms_norm.argtypes = [vp, vp, vp, vp, vp, i, i, i, i, i, f, i, cp, i]
+        lib.kh_qk_norm_rope.argtypes = [vp, vp, i, vp, vp, vp, vp, i, i, i, i, i, i, f, i, i, vp, vp, cp, i]
+        lib.kh_gemv.argtypes = [vp, vp, ctypes.POINTER(_WeightC), vp, i, i, i, i, i, vp, cp, i]
+        lib.kh_make_cond.argtypes = [vp, vp, vp, vp, vp, i, vp, cp, i]
+        lib.kh_gemm_f32.argtypes = [vp, vp, vp, vp, i, i, i, i, i, i, i, vp, cp, i]
+        lib.kh_rope_tables.argtypes = [i, i, i, i, vp, vp]
+        lib.kh_dit_layer_forward.argtypes = [vp, ctypes.POINTER(DitConfig), ctypes.POINTER(DitLayerC),
+                                             ctypes.POINTER(DitStateC), i, cp, i]
+        lib.kh_dit_forward.argtypes = [vp, ctypes.POINTER(DitConfig), ctypes.POINTER(DitLayerC), i,
+                                       ctypes.POINTER(DitStateC), i, cp, i]
+        for name in SYMBOLS[2:]:
+            getattr(lib, name).restype = i
         _lib = lib
     return _lib
 
@@ -134,3 +171,54 @@ def attention(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, O: torch.Tensor
                           ldv, ldo, group, int(causal), q_pos0, _ptr(G), ldg, _ptr(QB), _ptr(KB), err, 512)
     _check(rc, err)
     return O
+
+
+def _call(fn, *args):
+    err = ctypes.create_string_buffer(512)
+    rc = fn(*args, err, 512)
+    _check(rc, err)
+
+
+def rms_norm(x: torch.Tensor, mul: torch.Tensor, add: Optional[torch.Tensor], y: torch.Tensor, rows: int, width: int,
+             ld_in: int, ld_out: int, eps: float, center: int = 0):
+    """krea::Metal::rms_norm (engine/src/metal.h:72-74): y = norm(x) * mul (+ add); center = 1 -> LayerNorm."""
+    _call(load().kh_rms_norm, _stream(), _ptr(x), _ptr(mul), _ptr(add), _ptr(y), dtype_code(y.dtype), rows, width,
+          ld_in, ld_out, eps, center)
+    return y
+
+
+def qk_norm_rope(qkv: torch.Tensor, wq, wk, cos, sin, rows: int, ld: int, q_off: int, n_q: int, k_off: int, n_k: int,
+                 eps: float, rope_mode: int, big_dim: int = -1, qbig=None, kbig=None):
+    """krea::Metal::qk_norm_rope (engine/src/metal.h:77-79): per-head RMSNorm + RoPE in place."""
+    _call(load().kh_qk_norm_rope, _stream(), _ptr(qkv), dtype_code(qkv.dtype), _ptr(wq), _ptr(wk), _ptr(cos),
+          _ptr(sin), rows, ld, q_off, n_q, k_off, n_k, eps, rope_mode, big_dim, _ptr(qbig), _ptr(kbig))
+    return qkv
+
+
+def gemv(x: torch.Tensor, W: Weight, y: torch.Tensor, rows: int, N: int, K: int, ldw: int, act: int = 0, bias=None):
+    """gemv_bf16 semantics (engine/kernels/gemm.metal:346-371): y (+)= act(x) W~ + bias."""
+    wc = W.c()
+    _call(load().kh_gemv, _stream(), _ptr(x), ctypes.byref(wc), _ptr(y), rows, N, K, ldw, act, _ptr(bias))
+    return y
+
+
+def make_cond(tvec, table, n1, n2, D: int, mods):
+    """DiT::make_cond (engine/src/model.mm:317-347) for one layer, on the device."""
+    _call(load().kh_make_cond, _stream(), _ptr(tvec), _ptr(table), _ptr(n1), _ptr(n2), D, _ptr(mods))
+    return mods
+
+
+def gemm_f32(A, W, C, M: int, N: int, K: int, lda: int, ldw: int, ldc: int, mode: int, bias=None):
+    """krea::Metal::gemm_f32 (engine/src/metal.h:70-71): mode 1 bias, 2 GELU, 4 accumulate."""
+    _call(load().kh_gemm_f32, _stream(), _ptr(A), _ptr(W), _ptr(C), M, N, K, lda, ldw, ldc, mode, _ptr(bias))
+    return C
+
+
+def rope_tables(T: int, H: int, W: int, mode: int):
+    """Host RoPE tables (cos, sin) as float32 CPU tensors [T + H*W, 64]."""
+    R = T + H * W
+    c = torch.empty(R, 64, dtype=torch.float32)
+    s = torch.empty(R, 64, dtype=torch.float32)
+    if load().kh_rope_tables(T, H, W, mode, ctypes.c_void_p(c.data_ptr()), ctypes.c_void_p(s.data_ptr())) != 0:
+        raise KhError("rope_tables: bad arguments")
+    return c, s
