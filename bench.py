@@ -13,9 +13,10 @@ Reported beside it:
                  duration measured with HIP events on the launch stream, against 2.5 PFLOP/s dense fp16.
   cpu_baseline : the CPU oracle (fp32 dequant + fp32 GEMM + the same epilogues, OpenMP) on this host, timed
                  on the full pair once (rank 0, N = 1 only). A reported baseline, not a target.
-  dit_step_ms  : one full DiT denoising step at 1024^2 (4096 image + 512 text tokens) when --dit is given.
+  dit_step_ms  : one full DiT denoising step at 1024^2 (4096 image + 512 text tokens, 71 blocks = 12.06 B
+                 params of hidden 3072), the metric's second half (target < 500 ms).
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-dit] [--probe]
 """
 import argparse
 import json
@@ -32,6 +33,9 @@ M, D, FF = 4096, 3072, 12288
 PEAK_TFLOPS = 2500.0  # MI355X dense fp16 / bf16 MFMA
 FLOP_UP = 2.0 * M * D * FF
 FLOP_DOWN = 2.0 * M * FF * D
+# HBM bytes per up-projection launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, each scaled by the same
+# counter's reading for a 512 MiB copy (profiles/gemm_up_traffic_4096x3072x12288.md): 377.8 MB + 100.7 MB.
+UP_TRAFFIC_BYTES = 478.5e6
 
 
 def make_inputs(dev, seed=1234):
@@ -76,7 +80,10 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--dit", action="store_true", help="also time one full DiT step at 1024^2")
+    ap.add_argument("--no-dit", action="store_true", help="skip the full DiT step latency")
+    ap.add_argument("--probe", action="store_true",
+                    help="profiling probe: one up-projection launch and one 512 MiB device copy (for rocprofv3 "
+                         "--pmc FETCH_SIZE / WRITE_SIZE calibration), no JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the dequant-GEMM path has no multi-GPU mode in this build "
@@ -103,6 +110,14 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    if args.probe:
+        src = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        kh.gemm("gelu", X, Wup, H, M, FF, D, D, FF, FF)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        return
 
     # timed region: exactly `steps` steps, synchronized on both sides
     t0 = time.perf_counter()
@@ -143,12 +158,16 @@ def main():
         "pct_of_peak": round(100 * tflops / PEAK_TFLOPS, 2),
         "kernels_ms": {"up_gelu": round(up_ms, 4), "down_resid": round(down_ms, 4)},
         "roofline": {"bound": "mfma", "achieved": round(up_tflops, 2), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(up_tflops / PEAK_TFLOPS, 4), "traffic": None,
+                     "frac": round(up_tflops / PEAK_TFLOPS, 4), "traffic": UP_TRAFFIC_BYTES,
                      "kernel": "kh gemm_kernel<f16, int8 per-channel, GELU> (up-projection, 309.24 GFLOP/launch)"},
     }
-    if args.dit:
+    if not args.no_dit:
         from krea_image_amd import dit
-        out["dit_step_ms"] = dit.bench_step(dev, rows_img=4096, rows_txt=512)
+        step_info = dit.bench_step(dev, rows_img=4096, rows_txt=512, layers=71)
+        out["dit_step_ms"] = step_info["ms"]
+        out["dit_step"] = dict(step_info, workload="one full denoising step at 1024^2: 4096 image + 512 text "
+                               "tokens, 71 blocks of hidden 3072 / 24 heads / MLP x4 (12.06 B params, int8 "
+                               "per-channel), embed + adaLN + blocks + head", target_ms=500)
     if not args.no_cpu and int(os.environ.get("RANK", "0")) == 0:
         out["cpu_baseline"] = cpu_baseline(X, x, Wup, Wdown)
     print(json.dumps(out), flush=True)
