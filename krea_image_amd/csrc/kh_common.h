@@ -65,6 +65,29 @@ __host__ __device__ constexpr int waitcnt_imm(int vm, int lgkm) {
   return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | (lgkm << 8);
 }
 
+// Global loads the compiler does not track (inline asm): the caller orders them with explicit s_waitcnt and
+// vm_ready(), which ties the destination registers to the wait so no use can be hoisted above it. Used where
+// the compiler's own conservative vmcnt(0) (at loop back-edges) would cancel a multi-step prefetch.
+__device__ __forceinline__ uint32_t vm_load_b32(const void* p) {
+  uint32_t r;
+  asm volatile("global_load_dword %0, %1, off" : "=v"(r) : "v"(p));
+  return r;
+}
+__device__ __forceinline__ u32x2 vm_load_b64(const void* p) {
+  u32x2 r;
+  asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(r) : "v"(p));
+  return r;
+}
+__device__ __forceinline__ uint32_t vm_load_u16(const void* p) {
+  uint32_t r;
+  asm volatile("global_load_ushort %0, %1, off" : "=v"(r) : "v"(p));
+  return r;
+}
+template <typename T>
+__device__ __forceinline__ void vm_ready(T& r) {
+  asm volatile("" : "+v"(r));
+}
+
 // Workgroup barrier that is also a compiler memory barrier, without the release fence of __syncthreads
 // (which would also wait for LDS-direct loads still streaming in for later pipeline stages).
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }

@@ -70,20 +70,27 @@ __device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, const f
                                                   0);
 }
 
-// Raw weight registers of one thread for one K step: KR k-rows x 4 n-columns (+ the 4 column scales).
+// Raw weight registers of one thread for one K step: KR k-rows x 4 n-columns (+ the 4 column scales' raw
+// bits for the group format: f32, or f16 / bf16 in the low half).
 template <int WF, int KR>
 struct WRaw {
   uint32_t r[KR];
-  float s[4];
+  uint32_t s[4];
 };
 template <int KR>
 struct WRaw<WF_16, KR> {
   u32x2 r[KR];
 };
 
+__device__ __forceinline__ float scale_from_bits(uint32_t b, int s_dtype) {
+  if (s_dtype == KH_F32) return __builtin_bit_cast(float, b);
+  if (s_dtype == KH_BF16) return __builtin_bit_cast(float, b << 16);
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)b);
+}
+
 // Convert k-rows [8h, 8h+8) of column j to one 16-byte vector of 8 consecutive k (16-bit each).
 template <int ACT, int WF, int KR>
-__device__ __forceinline__ u32x4 convert_chunk(const WRaw<WF, KR>& w, int j, int h) {
+__device__ __forceinline__ u32x4 convert_chunk(const WRaw<WF, KR>& w, int j, int h, int s_dtype) {
   u32x4 out;
   if constexpr (WF == WF_16) {
     const uint32_t jj = (j & 1) * 2;
@@ -115,7 +122,7 @@ __device__ __forceinline__ u32x4 convert_chunk(const WRaw<WF, KR>& w, int j, int
     }
   } else {
     // group scales: round16(q * s) with the product rounded once in f32: fma(q + 128, s, -128 s)
-    const float s = w.s[j], nb = -128.0f * w.s[j];
+    const float s = scale_from_bits(w.s[j], s_dtype), nb = -128.0f * s;
 #pragma unroll
     for (int p = 0; p < 4; p++) {
       const uint32_t a = w.r[8 * h + 2 * p] ^ 0x80808080u, b = w.r[8 * h + 2 * p + 1] ^ 0x80808080u;
@@ -139,7 +146,7 @@ struct Cfg {
   static constexpr int KR = BK / WAVES;         // weight k-rows loaded per thread per K step
   static constexpr int WCH = 4 * (KR / 8);      // converted 16-byte weight chunks per thread per K step
   // loads issued per thread per K step, counted in the waits (a lower bound when group scales are loaded)
-  static constexpr int LOADS = X_LOADS + KR;
+  static constexpr int LOADS = X_LOADS + KR;    // + 4 scale loads for the group format
 };
 
 template <int ACT, int WF, int EPI, int WAVES>
@@ -185,19 +192,36 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
   constexpr int WB = (WF == WF_16) ? 2 : 1;
   const char* wbase = (const char*)p.W + ((size_t)(wave * KR) * p.ldw + wcol) * WB;
   const size_t wrow = (size_t)p.ldw * WB;
+  // untracked loads (see vm_load_b32): their waits are the explicit vmcnt of step() / the prologue
   auto issue_w = [&](int t, WRaw<WF, KR>& R) {
     const char* src = wbase + (size_t)(t * BK) * wrow;
 #pragma unroll
     for (int i = 0; i < KR; i++) {
       if constexpr (WF == WF_16)
-        R.r[i] = *(const u32x2*)(src + i * wrow);
+        R.r[i] = vm_load_b64(src + i * wrow);
       else
-        R.r[i] = *(const uint32_t*)(src + i * wrow);
+        R.r[i] = vm_load_b32(src + i * wrow);
     }
     if constexpr (WF == WF_I8_GROUP) {
       const size_t g = (size_t)((t * BK) / p.group) * p.ldw + wcol;
+      if (p.s_dtype == KH_F32) {
 #pragma unroll
-      for (int j = 0; j < 4; j++) R.s[j] = load_scale(p.S, p.s_dtype, g + j);
+        for (int j = 0; j < 4; j++) R.s[j] = vm_load_b32((const float*)p.S + g + j);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; j++) R.s[j] = vm_load_u16((const uint16_t*)p.S + g + j);
+      }
+    }
+  };
+  // raw(t) has landed: everything but the newest `newer` untracked / DMA loads is complete
+  auto ready_w = [&](WRaw<WF, KR>& R, auto newer_c) {
+    constexpr int NEWER = decltype(newer_c)::value;
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NEWER));
+#pragma unroll
+    for (int i = 0; i < KR; i++) vm_ready(R.r[i]);
+    if constexpr (WF == WF_I8_GROUP) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) vm_ready(R.s[j]);
     }
   };
   constexpr int H = KR / 8;  // k-chunks (8 rows) per column and thread
@@ -213,7 +237,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
     char* base = lds + (X_STAGES + stage) * STAGE;
 #pragma unroll
     for (int c = q * WCH / 4; c < (q + 1) * WCH / 4; c++)
-      *(u32x4*)(base + woff[c]) = convert_chunk<ACT, WF, KR>(R, c / H, c % H);
+      *(u32x4*)(base + woff[c]) = convert_chunk<ACT, WF, KR>(R, c / H, c % H, p.s_dtype);
   };
 
   // ---- MFMA operands: wave (wn, wm) owns n [128 wn, +128) x m [WME wm, +WME) = 4 x IB blocks of 32 x 32 ----
@@ -238,16 +262,19 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
   };
 
   const int nk = p.K / BK;
-  constexpr int LOADS = C_::LOADS;
+  constexpr int LOADS = C_::LOADS + (WF == WF_I8_GROUP ? 4 : 0);
+  using NewerT = std::integral_constant<int, LOADS>;
 
   // One K step: multiply stage t; convert raw(t + 1) into the other W stage between the MFMAs; the loads
   // of step t + 2 (activations straight into LDS, weights into Rl) are in flight meanwhile. Every step is
   // the same code: past the last step the loads re-fetch step nk - 1 into buffers nobody reads (stage
   // (t + 2) % 3 and the W stage of t + 1 are never the stage being multiplied), so the loop has no branches.
-  auto step = [&](int t, const WRaw<WF, KR>& Rc, WRaw<WF, KR>& Rl) {
+  auto step = [&](int t, WRaw<WF, KR>& Rc, WRaw<WF, KR>& Rl) {
     const int tl = min(t + 2, nk - 1);
     issue_x_to(tl, (t + 2) % X_STAGES);
     issue_w(tl, Rl);
+    // step t + 1's loads (issued one step ago: its activations into LDS and raw(t + 1) = Rc) have landed
+    ready_w(Rc, NewerT{});
     const char* xs = lds + (t % X_STAGES) * STAGE;
     const char* ws = lds + (X_STAGES + (t & 1)) * STAGE;
     u32x4 wf[2][4], xf[2][IB];
@@ -261,9 +288,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
         for (int ib = 0; ib < IB; ib++) acc[jb][ib] = mfma32<ACT>(wf[s & 1][jb], xf[s & 1][ib], acc[jb][ib]);
       store_w(Rc, (t + 1) & 1, s);
     }
-    // activations of step t + 1 must have landed: only this step's loads may still be outstanding
-    __builtin_amdgcn_s_waitcnt(waitcnt_imm(LOADS, 15));
-    lds_barrier();
+    lds_barrier();  // this step's converted weights and (waited above) step t + 1's activations are visible
   };
 
   WRaw<WF, KR> R0, R1;
@@ -271,7 +296,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
   issue_w(0, R0);
   issue_x_to(min(1, nk - 1), 1);
   issue_w(min(1, nk - 1), R1);
-  __builtin_amdgcn_s_waitcnt(waitcnt_imm(LOADS, 15));
+  ready_w(R0, NewerT{});
 #pragma unroll
   for (int q = 0; q < 4; q++) store_w(R0, 0, q);
   lds_barrier();
@@ -281,8 +306,11 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
     step(t + 1, R0, R1);
   }
   if (t < nk) step(t, R1, R0);
-  // the re-fetches issued by the last steps must land before the LDS is reused below
-  __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
+  // The last steps' re-fetches must land before the LDS is reused below. The raw registers they target are
+  // never read, so they are tied here, after the wait: otherwise the compiler would hand those registers to
+  // other values while the (untracked) loads are still in flight and the loads would overwrite them.
+  ready_w(R0, std::integral_constant<int, 0>{});
+  ready_w(R1, std::integral_constant<int, 0>{});
   lds_barrier();
 
   // ---- epilogue. The LDS is free after the last barrier: the block's 256 column scales and vec entries
