@@ -82,10 +82,17 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__
 
 // ------------------------------------------------------------------------------------------------------
 // Per-head RMSNorm (weight [128]) + RoPE, in place on a 16-bit fused projection buffer:
-// engine/kernels/norm.metal:81-134. One wave per (row, head); lane i owns the two channels of rotation
-// pair i: (2i, 2i + 1) for rope_mode 0 (interleaved pairs), (i, i + 64) for rope_mode 1 (rotate-half) and
-// for rope_mode 2 (no rotation). cos / sin: f32 [rows, 64]. big_dim >= 0: that dimension's rotated value
-// goes to qbig [rows, n_q] / kbig [rows, n_k] in f32 and is zeroed in the buffer.
+// engine/kernels/norm.metal:81-134. 16 lanes per (row, head), 8 consecutive channels (one 16-byte load) per
+// lane, 4 heads per wave; the sum of squares is reduced over the 16 lanes. rope_mode 0: interleaved pairs
+// (2i, 2i + 1) -- the lane's 4 pairs are local; rope_mode 1: rotate-half (i, i + 64) -- the partner channels
+// sit in lane ^ 8; rope_mode 2: no rotation. cos / sin: f32 [rows, 64]. big_dim >= 0: that dimension's
+// rotated value goes to qbig [rows, n_q] / kbig [rows, n_k] in f32 and is zeroed in the buffer.
+__device__ __forceinline__ float sum16(float v) {
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
 template <int DT>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(uint16_t* __restrict__ qkv, const float* __restrict__ wq,
                                                            const float* __restrict__ wk, const float* __restrict__ cosb,
@@ -93,59 +100,81 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(uint16_t* __restrict_
                                                            int n_q, int k_off, int n_k, float eps, int rope_mode,
                                                            int big_dim, float* __restrict__ qbig,
                                                            float* __restrict__ kbig) {
-  const int unit = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const long unit = (long)blockIdx.x * 16 + (threadIdx.x >> 4);  // (row, head) pair
+  const int sl = threadIdx.x & 15;                                 // lane within the head: channels 8 sl .. 8 sl + 7
   const int heads = n_q + n_k;
-  const int row = unit / heads, hh = unit % heads;
-  if (row >= rows) return;
+  const int row = (int)(unit / heads), hh = (int)(unit % heads);
+  const bool valid = row < rows;
+  const int rr = valid ? row : rows - 1;
   const bool is_q = hh < n_q;
   const int col = is_q ? q_off + hh * 128 : k_off + (hh - n_q) * 128;
-  uint16_t* base = qkv + (size_t)row * ld + col;
-  const float* w = is_q ? wq : wk;
-  const int c0 = rope_mode == 0 ? 2 * lane : lane, c1 = rope_mode == 0 ? 2 * lane + 1 : lane + 64;
-  float x0, x1;
-  if (rope_mode == 0) {
-    const uint32_t pr = *(const uint32_t*)(base + c0);
-    x0 = from16<DT>((uint16_t)pr);
-    x1 = from16<DT>((uint16_t)(pr >> 16));
-  } else {
-    x0 = from16<DT>(base[c0]);
-    x1 = from16<DT>(base[c1]);
+  uint16_t* base = qkv + (size_t)rr * ld + col + sl * 8;
+  const float* w = (is_q ? wq : wk) + sl * 8;
+  const u32x4 raw = *(const u32x4*)base;
+  float x[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) x[e] = from16<DT>((uint16_t)(raw[e >> 1] >> (16 * (e & 1))));
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; e++) ss += x[e] * x[e];
+  const float rrms = rsqrtf(sum16(ss) * (1.0f / 128.0f) + eps);
+  const f32x4 w0 = *(const f32x4*)w, w1 = *(const f32x4*)(w + 4);
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    x[e] *= rrms * w0[e];
+    x[e + 4] *= rrms * w1[e];
   }
-  const float rrms = rsqrtf(wave_sum(x0 * x0 + x1 * x1) * (1.0f / 128.0f) + eps);
-  x0 *= rrms * w[c0];
-  x1 *= rrms * w[c1];
-  float o0 = x0, o1 = x1;
-  if (rope_mode != 2) {
-    const float c = cosb[(size_t)row * 64 + lane], s = sinb[(size_t)row * 64 + lane];
-    o0 = x0 * c - x1 * s;
-    o1 = x0 * s + x1 * c;
-  }
-  if (big_dim >= 0) {
-    float* dst = is_q ? qbig + (size_t)row * n_q + hh : kbig + (size_t)row * n_k + (hh - n_q);
-    if (c0 == big_dim) {
-      *dst = o0;
-      o0 = 0.f;
-    } else if (c1 == big_dim) {
-      *dst = o1;
-      o1 = 0.f;
+  float o[8];
+  if (rope_mode == 0) {  // pairs 4 sl .. 4 sl + 3 at frequencies of the same index
+    const f32x4 c = *(const f32x4*)(cosb + (size_t)rr * 64 + sl * 4), s = *(const f32x4*)(sinb + (size_t)rr * 64 + sl * 4);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      o[2 * i] = x[2 * i] * c[i] - x[2 * i + 1] * s[i];
+      o[2 * i + 1] = x[2 * i] * s[i] + x[2 * i + 1] * c[i];
     }
-  }
-  if (rope_mode == 0) {
-    *(uint32_t*)(base + c0) = (uint32_t)to16<DT>(o0) | ((uint32_t)to16<DT>(o1) << 16);
+  } else if (rope_mode == 1) {  // channel i pairs with i + 64 (lane ^ 8), frequency i % 64
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) y[e] = __shfl_xor(x[e], 8);
+    const int f = (sl & 7) * 8;
+    const f32x4 c0 = *(const f32x4*)(cosb + (size_t)rr * 64 + f), c1 = *(const f32x4*)(cosb + (size_t)rr * 64 + f + 4);
+    const f32x4 s0 = *(const f32x4*)(sinb + (size_t)rr * 64 + f), s1 = *(const f32x4*)(sinb + (size_t)rr * 64 + f + 4);
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const float c = e < 4 ? c0[e] : c1[e - 4], s = e < 4 ? s0[e] : s1[e - 4];
+      o[e] = sl < 8 ? x[e] * c - y[e] * s : x[e] * c + y[e] * s;
+    }
   } else {
-    base[c0] = to16<DT>(o0);
-    base[c1] = to16<DT>(o1);
+#pragma unroll
+    for (int e = 0; e < 8; e++) o[e] = x[e];
   }
+  if (!valid) return;
+  if (big_dim >= 0 && big_dim / 8 == sl) {
+    const int e = big_dim % 8;
+    float v = o[0];
+#pragma unroll
+    for (int i = 1; i < 8; i++)
+      if (i == e) v = o[i];
+    if (is_q) qbig[(size_t)row * n_q + hh] = v;
+    else kbig[(size_t)row * n_k + (hh - n_q)] = v;
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+      if (i == e) o[i] = 0.f;
+  }
+  u32x4 out;
+#pragma unroll
+  for (int i = 0; i < 4; i++) out[i] = (uint32_t)to16<DT>(o[2 * i]) | ((uint32_t)to16<DT>(o[2 * i + 1]) << 16);
+  *(u32x4*)base = out;
 }
 
 // ------------------------------------------------------------------------------------------------------
 // adaLN modulation GEMV: y[r, n] (+)= sum_k act(x[r, k]) W~[k, n] (+ bias[n]), rows <= 4, x / y f32.
 // engine/kernels/gemm.metal:346-371 (gemv_bf16: act bit 0 = SiLU on load, bit 1 = accumulate) with the
-// weight formats of kh_gemm. HBM-bound (the int8 weight is read once): grid (N / 256, KSPLIT); each
-// workgroup reads a K / KSPLIT x 256 slab with one dword (4 columns) per lane and row, coalesced 256 B per
-// wave; its 4 waves split the slab's rows, reduce through LDS and add into y with one f32 atomic per
-// column. y is initialised (bias, or 0, or left for accumulation) by gemv_init before the split kernel.
-constexpr int GEMV_COLS = 256, GEMV_KSPLIT_MAX = 32;
+// weight formats of kh_gemm. HBM-bound (each weight byte is read once): grid (N / COLS, KSPLIT); a lane owns
+// 16 consecutive bytes of a weight row (16 int8 columns, or 8 16-bit ones), so a wave reads 1 KB per row;
+// the 4 waves split the slab's rows, each keeping 8 rows' loads in flight, reduce through LDS and add into y
+// with one f32 atomic per column. y is initialised (bias, or 0, or kept for accumulation) by gemv_init.
+constexpr int GEMV_KSPLIT_MAX = 64;
 
 __global__ void gemv_init(float* y, const float* bias, int rows, int N, int ldy, int accumulate) {
   const int n = blockIdx.x * blockDim.x + threadIdx.x;
@@ -157,61 +186,86 @@ __global__ void gemv_init(float* y, const float* bias, int rows, int N, int ldy,
   }
 }
 
-template <int WF>  // 0: 16-bit weights (WD = dtype), 1: int8 per-channel, 2: int8 group
+template <int WF>  // 0: 16-bit weights (8 columns per lane), 1: int8 per-channel, 2: int8 group (16 per lane)
 __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, const void* __restrict__ W,
                                                    const void* __restrict__ S, int s_dtype, int group, int w16_dtype,
                                                    float* __restrict__ y, int rows, int N, int K, int ldw, int ldy,
                                                    int silu, int kchunk) {
-  __shared__ float xs[4][1024];        // activated x of this slab (rows x kchunk), kchunk <= 1024
-  __shared__ f32x4 part[4][4][64];     // [wave][row][lane]
+  constexpr int CPL = WF == 0 ? 8 : 16;  // columns per lane
+  constexpr int COLS = 16 * CPL;         // 16 lanes span the block's columns; lane >> 4 picks a row group
+  __shared__ float xs[4][512];           // activated x of this slab (rows x kchunk), kchunk <= 512
+  __shared__ float part[16][4][COLS];    // [row group][row][column]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int n = blockIdx.x * GEMV_COLS + lane * 4;
+  const int rg = wave * 4 + (lane >> 4);  // 16 row groups
+  const int n = blockIdx.x * COLS + (lane & 15) * CPL;
   const int k0 = blockIdx.y * kchunk, k1 = min(K, k0 + kchunk);
   for (int i = tid; i < rows * (k1 - k0); i += 256) {
     const int r = i / (k1 - k0), k = i % (k1 - k0);
-    float v = x[(size_t)r * K + k0 + k];
+    const float v = x[(size_t)r * K + k0 + k];
     xs[r][k] = silu ? silu_f(v) : v;
   }
   __syncthreads();
-  f32x4 acc[4] = {};
+  float acc[4][CPL];
+#pragma unroll
+  for (int r = 0; r < 4; r++)
+#pragma unroll
+    for (int c = 0; c < CPL; c++) acc[r][c] = 0.f;
   if (n < N) {
-    for (int k = k0 + wave; k < k1; k += 4) {
-      float w4[4];
-      if (WF == 0) {
-        const u32x2 raw = *(const u32x2*)((const uint16_t*)W + (size_t)k * ldw + n);
+    const char* wp = (const char*)W + ((size_t)n) * (WF == 0 ? 2 : 1);
+    const size_t row_bytes = (size_t)ldw * (WF == 0 ? 2 : 1);
+    for (int kb = k0 + rg; kb < k1; kb += 16 * 8) {
+      u32x4 raw[8];
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const uint16_t hbits = (uint16_t)(raw[e >> 1] >> (16 * (e & 1)));
-          w4[e] = w16_dtype == KH_BF16 ? from16<KH_BF16>(hbits) : from16<KH_F16>(hbits);
-        }
-      } else {
-        const uint32_t raw = *(const uint32_t*)((const int8_t*)W + (size_t)k * ldw + n);
-#pragma unroll
-        for (int e = 0; e < 4; e++) w4[e] = (float)(int8_t)(raw >> (8 * e));
-        if (WF == 2) {
-#pragma unroll
-          for (int e = 0; e < 4; e++) w4[e] *= load_scale(S, s_dtype, (size_t)(k / group) * ldw + n + e);
-        }
+      for (int u = 0; u < 8; u++) {
+        const int k = kb + 16 * u;
+        raw[u] = k < k1 ? *(const u32x4*)(wp + (size_t)k * row_bytes) : (u32x4){0u, 0u, 0u, 0u};
       }
-      for (int r = 0; r < rows; r++) {
-        const float xv = xs[r][k - k0];
 #pragma unroll
-        for (int e = 0; e < 4; e++) acc[r][e] += xv * w4[e];
+      for (int u = 0; u < 8; u++) {
+        const int k = kb + 16 * u;
+        if (k >= k1) break;
+        float wv[CPL];
+        if (WF == 0) {
+#pragma unroll
+          for (int c = 0; c < 8; c++) {
+            const uint16_t hb = (uint16_t)(raw[u][c >> 1] >> (16 * (c & 1)));
+            wv[c] = w16_dtype == KH_BF16 ? from16<KH_BF16>(hb) : from16<KH_F16>(hb);
+          }
+        } else {
+#pragma unroll
+          for (int c = 0; c < 16; c++) wv[c] = (float)(int8_t)(raw[u][c >> 2] >> (8 * (c & 3)));
+          if (WF == 2) {
+            const size_t g = (size_t)(k / group) * ldw + n;
+#pragma unroll
+            for (int c = 0; c < 16; c++) wv[c] *= load_scale(S, s_dtype, g + c);
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) {  // static indices keep acc in registers
+          if (r >= rows) break;
+          const float xv = xs[r][k - k0];
+#pragma unroll
+          for (int c = 0; c < CPL; c++) acc[r][c] += xv * wv[c];
+        }
       }
     }
   }
-  for (int r = 0; r < rows; r++) part[wave][r][lane] = acc[r];
-  __syncthreads();
-  if (wave == 0 && n < N) {
-    for (int r = 0; r < rows; r++) {
-      f32x4 s = part[0][r][lane] + part[1][r][lane] + part[2][r][lane] + part[3][r][lane];
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        float v = s[e];
-        if (WF == 1) v *= load_scale(S, s_dtype, n + e);
-        atomicAdd(y + (size_t)r * ldy + n + e, v);
-      }
-    }
+  for (int r = 0; r < 4; r++) {
+    if (r >= rows) break;
+#pragma unroll
+    for (int c = 0; c < CPL; c++) part[rg][r][(lane & 15) * CPL + c] = acc[r][c];
+  }
+  __syncthreads();
+  for (int i = tid; i < rows * COLS; i += 256) {
+    const int r = i / COLS, c = i % COLS;
+    const int nc = blockIdx.x * COLS + c;
+    if (nc >= N) continue;
+    float v = 0.f;
+#pragma unroll
+    for (int g = 0; g < 16; g++) v += part[g][r][c];
+    if (WF == 1) v *= load_scale(S, s_dtype, nc);
+    atomicAdd(y + (size_t)r * ldy + nc, v);
   }
 }
 
@@ -237,21 +291,33 @@ __global__ void make_cond_kernel(const float* tvec, const float* table, const fl
 // fp32 GEMM of the patch embed (64 -> D) and the final projection (D -> 64): engine/kernels/f32gemm.metal
 // (gemm_f32w) with its modes bit 0 bias, bit 1 GELU(tanh), bit 2 accumulate. 64 x 64 tiles, 256 threads,
 // 4 x 4 outputs per thread, K staged 16 at a time through LDS. Tiny next to the DiT layers.
+// Split-K form (gridDim.z > 1, no GELU): each z-slice adds its partial product into C with f32 atomics after
+// gemm_f32_init has set C to bias / 0 (or kept it, for accumulate).
+__global__ void gemm_f32_init(float* C, const float* bias, int M, int N, int ldc, int mode) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x, m = blockIdx.y;
+  if (n >= N) return;
+  float* cp = C + (size_t)m * ldc + n;
+  const float b = (mode & 1) ? bias[n] : 0.f;
+  *cp = (mode & 4) ? *cp + b : b;
+}
+
 __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ W,
                                                        float* __restrict__ C, const float* __restrict__ bias, int M,
                                                        int N, int K, int lda, int ldw, int ldc, int mode) {
+  const int kz = gridDim.z > 1 ? (K + gridDim.z - 1) / gridDim.z : K;
+  const int kbeg = blockIdx.z * kz, kfin = min(K, kbeg + kz);
   __shared__ float As[16][64 + 1];
   __shared__ float Ws[16][64];
   const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
   const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
   float acc[4][4] = {};
-  for (int k0 = 0; k0 < K; k0 += 16) {
+  for (int k0 = kbeg; k0 < kfin; k0 += 16) {
     for (int i = tid; i < 16 * 64; i += 256) {
       const int r = i / 16, c = i % 16;  // A tile: 64 rows x 16 k
       const int m = m0 + r, k = k0 + c;
-      As[c][r] = (m < M && k < K) ? A[(size_t)m * lda + k] : 0.f;
+      As[c][r] = (m < M && k < kfin) ? A[(size_t)m * lda + k] : 0.f;
       const int kr = i / 64, nc = i % 64;  // W tile: 16 k x 64 cols
-      Ws[kr][nc] = (k0 + kr < K && n0 + nc < N) ? W[(size_t)(k0 + kr) * ldw + n0 + nc] : 0.f;
+      Ws[kr][nc] = (k0 + kr < kfin && n0 + nc < N) ? W[(size_t)(k0 + kr) * ldw + n0 + nc] : 0.f;
     }
     __syncthreads();
 #pragma unroll
@@ -277,9 +343,13 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
       const int n = n0 + tx * 4 + j;
       if (n >= N) continue;
       float v = acc[i][j];
+      float* cp = C + (size_t)m * ldc + n;
+      if (gridDim.z > 1) {
+        atomicAdd(cp, v);
+        continue;
+      }
       if (mode & 1) v += bias[n];
       if (mode & 2) v = gelu_tanh_f(v);
-      float* cp = C + (size_t)m * ldc + n;
       *cp = (mode & 4) ? *cp + v : v;
     }
   }
@@ -324,8 +394,10 @@ int qk_norm_rope(hipStream_t st, void* qkv, int dtype, const float* wq, const fl
   if (!qkv || (n_q && !wq) || (n_k && !wk)) return e.fail("qk_norm_rope: null buffer / weight");
   if (big_dim >= 128 || (big_dim >= 0 && (!qbig || !kbig))) return e.fail("qk_norm_rope: big_dim needs qbig / kbig");
   if (ld % 2 || q_off % 2 || k_off % 2) return e.fail("qk_norm_rope: offsets must be even");
+  if (ld % 8 || q_off % 8 || k_off % 8 || ((uintptr_t)qkv & 15))
+    return e.fail("qk_norm_rope: rows and head offsets must be 16-byte aligned");
   const long units = (long)rows * (n_q + n_k);
-  dim3 grid((unsigned)((units + 3) / 4)), block(256);
+  dim3 grid((unsigned)((units + 15) / 16)), block(256);
   if (dtype == KH_F16)
     hipLaunchKernelGGL(qk_norm_rope_kernel<KH_F16>, grid, block, 0, st, (uint16_t*)qkv, wq, wk, cosb, sinb, rows, ld,
                        q_off, n_q, k_off, n_k, eps, rope_mode, big_dim, qbig, kbig);
@@ -339,7 +411,7 @@ int qk_norm_rope(hipStream_t st, void* qkv, int dtype, const float* wq, const fl
 int gemv(hipStream_t st, const float* x, const kh_weight& W, float* y, int rows, int N, int K, int ldw, int act,
          const float* bias, Err& e) {
   if (rows <= 0 || rows > 4 || N <= 0 || K <= 0) return e.fail("gemv: rows must be 1..4 and N, K > 0");
-  if (N % 4 || ldw % 4 || ldw < N) return e.fail("gemv: N and ldw must be multiples of 4, ldw >= N");
+  if (ldw < N) return e.fail("gemv: ldw %d < N %d", ldw, N);
   if (!x || !W.w || !y) return e.fail("gemv: null x / W / y");
   int wf, group = K;
   if (W.w_dtype == KH_I8) {
@@ -352,12 +424,14 @@ int gemv(hipStream_t st, const float* x, const kh_weight& W, float* y, int rows,
   } else {
     return e.fail("gemv: weight dtype must be int8, f16 or bf16");
   }
-  // K split so the grid has >= ~512 workgroups; each slab's x fits the 1024-entry LDS stage
-  const int col_blocks = (N + GEMV_COLS - 1) / GEMV_COLS;
+  // K split so the grid has >= ~512 workgroups; each slab's x fits the 512-entry LDS stage
+  const int cols = wf == 0 ? 128 : 256;
+  if (N % (wf == 0 ? 8 : 16) || ldw % 16) return e.fail("gemv: N must be a multiple of 16 (8 for 16-bit), ldw of 16");
+  const int col_blocks = (N + cols - 1) / cols;
   int ksplit = 1;
-  while (ksplit < GEMV_KSPLIT_MAX && (col_blocks * ksplit < 512 || (K + ksplit - 1) / ksplit > 1024)) ksplit *= 2;
-  int kchunk = (K + ksplit - 1) / ksplit;
-  if (kchunk > 1024) return e.fail("gemv: K %d too large", K);
+  while (ksplit < GEMV_KSPLIT_MAX && (col_blocks * ksplit < 512 || (K + ksplit - 1) / ksplit > 512)) ksplit *= 2;
+  const int kchunk = (K + ksplit - 1) / ksplit;
+  if (kchunk > 512) return e.fail("gemv: K %d too large", K);
   hipLaunchKernelGGL(gemv_init, dim3((N + 255) / 256), dim3(256), 0, st, y, bias, rows, N, N, (act & 2) ? 1 : 0);
   dim3 grid(col_blocks, (K + kchunk - 1) / kchunk), block(256);
   if (wf == 0)
@@ -387,6 +461,12 @@ int gemm_f32(hipStream_t st, const float* A, const float* W, float* C, int M, in
   if (!A || !W || !C || ((mode & 1) && !bias)) return e.fail("gemm_f32: null A / W / C (or bias for mode & 1)");
   if (lda < K || ldw < N || ldc < N) return e.fail("gemm_f32: bad strides");
   dim3 grid((N + 63) / 64, (M + 63) / 64), block(256);
+  // small grids with long K (the D -> 64 head) split K over workgroups; GELU needs the full sum
+  int ksplit = 1;
+  while (!(mode & 2) && grid.x * grid.y * ksplit < 512 && K / (ksplit * 2) >= 128) ksplit *= 2;
+  grid.z = ksplit;
+  if (ksplit > 1)
+    hipLaunchKernelGGL(gemm_f32_init, dim3((N + 255) / 256, M), dim3(256), 0, st, C, bias, M, N, ldc, mode);
   hipLaunchKernelGGL(gemm_f32_kernel, grid, block, 0, st, A, W, C, bias, M, N, K, lda, ldw, ldc, mode);
   const hipError_t r = hipGetLastError();
   return r == hipSuccess ? KH_OK : e.hip(r, "gemm_f32 launch");
