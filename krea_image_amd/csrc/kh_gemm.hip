@@ -70,6 +70,10 @@ __device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, const f
                                                   0);
 }
 
+#ifndef SCHED_FENCE
+#define SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
+#endif
+
 // Raw weight registers of one thread for one K step: KR k-rows x 4 n-columns (+ the 4 column scales' raw
 // bits for the group format: f32, or f16 / bf16 in the low half).
 template <int WF, int KR>
@@ -281,12 +285,17 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
     read_frags(xs, ws, 0, wf[0], xf[0]);
 #pragma unroll
     for (int s = 0; s < 4; s++) {
+      // Scheduling regions: the next slice's fragment reads are issued first and may not sink past the
+      // region end, so they have a whole slice of MFMAs (this wave's and the other wave's on the SIMD) to
+      // land; left alone, the scheduler places them ~4 MFMAs before use and then waits for them.
       if (s < 3) read_frags(xs, ws, s + 1, wf[(s + 1) & 1], xf[(s + 1) & 1]);
+      SCHED_FENCE();
 #pragma unroll
       for (int jb = 0; jb < 4; jb++)
 #pragma unroll
         for (int ib = 0; ib < IB; ib++) acc[jb][ib] = mfma32<ACT>(wf[s & 1][jb], xf[s & 1][ib], acc[jb][ib]);
       store_w(Rc, (t + 1) & 1, s);
+      SCHED_FENCE();
     }
     lds_barrier();  // this step's converted weights and (waited above) step t + 1's activations are visible
   };
