@@ -5,7 +5,9 @@
 // engine/src/metal.mm:193-202 (Metal::attention):
 //   O[q, h] = softmax_k(Q[q, h] . K[k, h / group] / sqrt(128) (+ QB[q, h] KB[k, h / group])) V[k, h / group]
 //             (* sigmoid(G[q, h]) when a gate is given), optional causal mask key <= q + q_pos0.
-// P is rounded to the 16-bit type before P V (attention.metal:272-276); row sums use the unrounded p.
+// P is rounded to the 16-bit type before P V (attention.metal:272-276). The row sums here add the same
+// rounded P (one v_dot2 per key pair) where the reference adds the unrounded p: numerator and denominator
+// then see identical weights; the difference is below half a 16-bit ulp per term, unbiased.
 //
 // Design (CDNA4, v_mfma_f32_32x32x16):
 //  * Transposed products: S^T = K Q^T (K is the A operand straight from LDS, Q^T the B operand held in
@@ -52,6 +54,27 @@ __device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, const f
   else
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
                                                   0);
+}
+
+// two f32 -> packed 16-bit (round to nearest even)
+template <int DT>
+__device__ __forceinline__ uint32_t pack16(float a, float b) {
+  if constexpr (DT == KH_BF16) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, (bf2){(__bf16)a, (__bf16)b});  // v_cvt_pk_bf16_f32
+  } else {
+    return (uint32_t)to16<DT>(a) | ((uint32_t)to16<DT>(b) << 16);
+  }
+}
+// acc + lo + hi of a packed 16-bit pair (v_dot2c_f32_{f16,bf16} against (1, 1))
+template <int DT>
+__device__ __forceinline__ float dot2_ones(uint32_t pr, float acc) {
+  if constexpr (DT == KH_BF16) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, pr), (bf2){(__bf16)1.0f, (__bf16)1.0f}, acc, false);
+  } else {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pr), (f16x2){(_Float16)1.0f, (_Float16)1.0f}, acc, false);
+  }
 }
 
 __device__ __forceinline__ int vt_chunk(int d, int kc) { return kc ^ (d & 7) ^ ((d >> 3) & 7); }
@@ -161,7 +184,7 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
       }
     }
 
-    // scores in log2 units, masking, block max
+    // block max on the raw scores (the positive scale commutes with max); masked scores are -inf
     const int key0 = b * BKEYS;
     const bool need_mask = CAUSAL || (key0 + BKEYS > p.Lk);
     float bmax = -INFINITY;
@@ -172,7 +195,6 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
         const int kl = kh * 32 + (i >> 2) * 8 + hh * 4 + (i & 3);
         float s = st[kh][i];
         if (BIG) s += qb * kb_s[cur][kl];
-        s *= p.scale_log2;
         if (need_mask) {
           const int key = key0 + kl;
           if (key >= p.Lk || (CAUSAL && key > q + p.q_pos0)) s = -INFINITY;
@@ -180,10 +202,9 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
         st[kh][i] = s;
         bmax = fmaxf(bmax, s);
       }
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
-    // lazy max update: only when some query of the wave grew by more than LAZY_TH
-    const bool grow = bmax > m + LAZY_TH;
-    if (__any(grow)) {
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32)) * p.scale_log2;
+    // lazy max update (log2 units): only when some query of the wave grew by more than LAZY_TH
+    if (__any(bmax > m + LAZY_TH)) {
       const float m_new = fmaxf(m, bmax);
       const float alpha = __builtin_amdgcn_exp2f(m - m_new);
       m = m_new;
@@ -192,16 +213,17 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
       for (int db = 0; db < 4; db++) o[db] *= alpha;
     }
 
-    // P^T = exp2(s - m) as the 16-bit B operand of O^T += V^T P^T; key step j uses st[j / 2][8 (j & 1) ..]
+    // P^T = exp2(s * scale_log2 - m) as the 16-bit B operand of O^T += V^T P^T (key step j uses
+    // st[j / 2][8 (j & 1) ..]); the row sum accumulates the rounded P with v_dot2 (2 keys per op)
     u32x4 pf[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        const float p0 = __builtin_amdgcn_exp2f(st[j >> 1][(j & 1) * 8 + 2 * e] - m);
-        const float p1 = __builtin_amdgcn_exp2f(st[j >> 1][(j & 1) * 8 + 2 * e + 1] - m);
-        l += p0 + p1;
-        pf[j][e] = (uint32_t)to16<DT>(p0) | ((uint32_t)to16<DT>(p1) << 16);
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[j >> 1][(j & 1) * 8 + 2 * e], p.scale_log2, -m));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[j >> 1][(j & 1) * 8 + 2 * e + 1], p.scale_log2, -m));
+        pf[j][e] = pack16<DT>(p0, p1);
+        l = dot2_ones<DT>(pf[j][e], l);
       }
     }
 #pragma unroll
