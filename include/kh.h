@@ -132,9 +132,11 @@ typedef struct kh_dit_layer {
   kh_weight o;            /* [D, D] */
   kh_weight up;           /* [D, ff] (GELU) or [D, 2 ff] interleaved (SwiGLU) */
   kh_weight down;         /* [ff, D] */
-  kh_weight ada;          /* adaLN linear [cond_dim, 6 D]; ada.w == NULL: the caller fills state->mods */
+  kh_weight ada;          /* adaLN linear [cond_dim, 6 D] (per-layer adaLN, the benchmark configs), or w == NULL */
   const float* ada_bias;  /* [6 D] or NULL */
-  const float* mod_table; /* [6 D] per-layer table added to the adaLN output, or NULL */
+  const float* mod_table; /* [6 D] per-layer table added to tvec, or NULL. ada.w == NULL and mod_table != NULL:
+                             mods = make_cond(state->tvec, mod_table, n1, n2) from the step's shared tvec (the
+                             reference, `L{i}.mod`); both NULL: the caller fills state->mods */
   const float* n1;        /* [D] pre-attention norm weight (stored as 1 + w) */
   const float* n2;        /* [D] pre-MLP norm weight */
   const float* qn;        /* [128] q norm weight */
@@ -165,6 +167,44 @@ int kh_dit_layer_forward(kh_stream stream, const kh_dit_config* cfg, const kh_di
 /* Layers [0, n_layers) in order (engine/src/model.mm:519-525, DiT::run_layers). */
 int kh_dit_forward(kh_stream stream, const kh_dit_config* cfg, const kh_dit_layer* layers, int n_layers,
                    const kh_dit_state* state, int rows, char* err, int errlen);
+
+/* ---- packed weight files (.qw) ----
+ * Format of tools/convert.py:13-17,49-89: "QWTS" | u32 version | u64 header_len | JSON header | pad | data,
+ * tensors 16 KiB aligned. kh_qw_open maps and validates a file (WeightFile::WeightFile,
+ * engine/src/weights.mm:16-79); kh_qw_find is WeightFile::info / get (engine/src/weights.mm:88-98); kh_qw_upload copies
+ * the data region once into one resident device allocation (replaces the no-copy Metal buffers of
+ * weights.mm:59-68; a discrete GPU needs the bytes in HBM). Tensor device address = base + file offset. */
+#define KH_QW_MAX_DIMS 8
+typedef struct kh_qw kh_qw;
+typedef struct kh_qw_tensor {
+  const char* name;                 /* valid until kh_qw_close */
+  int dtype;                        /* KH_F32 / KH_F16 / KH_BF16 / KH_I8 */
+  int ndim;
+  int64_t shape[KH_QW_MAX_DIMS];
+  size_t offset;                    /* from the data start */
+  size_t nbytes;
+  const void* host;                 /* into the read-only mapping */
+  void* dev;                        /* device copy after kh_qw_upload, else NULL */
+} kh_qw_tensor;
+/* NULL on error (message in err). */
+kh_qw* kh_qw_open(const char* path, char* err, int errlen);
+void kh_qw_close(kh_qw* f);                                      /* also frees the device copy */
+int kh_qw_count(const kh_qw* f);
+unsigned kh_qw_version(const kh_qw* f);
+const char* kh_qw_meta(const kh_qw* f);                          /* the header's "meta" object as JSON text */
+int kh_qw_at(const kh_qw* f, int i, kh_qw_tensor* out);          /* i-th tensor in name order */
+int kh_qw_find(const kh_qw* f, const char* name, kh_qw_tensor* out); /* KH_EINVAL if absent */
+/* Synchronous: returns once the data is resident on the current device. Idempotent. */
+int kh_qw_upload(kh_qw* f, kh_stream stream, char* err, int errlen);
+
+/* ---- runtime surface around the ops (Metal::alloc / begin / wait, engine/src/metal.h:53-60) ---- */
+int kh_stream_create(kh_stream* out, char* err, int errlen);  /* non-blocking stream, default priority */
+int kh_stream_destroy(kh_stream s);
+int kh_stream_sync(kh_stream s, char* err, int errlen);       /* Metal::wait */
+int kh_alloc(void** out, size_t bytes, char* err, int errlen);/* hipMalloc; Metal::alloc */
+int kh_free(void* p);
+int kh_upload(kh_stream s, void* dst, const void* src, size_t bytes, char* err, int errlen);   /* H2D, synchronous */
+int kh_download(kh_stream s, void* dst, const void* src, size_t bytes, char* err, int errlen); /* D2H, synchronous */
 
 /* Library identification (for the loader checks of the host bindings). */
 const char* kh_version(void);

@@ -40,6 +40,11 @@ int dit_layer_forward(hipStream_t st, const kh_dit_config& c, const kh_dit_layer
     if (!s.cond || !s.tvec) return e.fail("dit: adaLN needs state->cond and state->tvec");
     if ((rc = gemv(st, s.cond, L.ada, s.tvec, 1, 6 * D, s.cond_dim, 6 * D, 1, L.ada_bias, e))) return rc;
     if ((rc = make_cond(st, s.tvec, L.mod_table, L.n1, L.n2, D, s.mods, e))) return rc;
+  } else if (L.mod_table) {
+    // the reference's layout: one tvec per step (Conditioning::compute, model.mm:571-591) shared by all
+    // layers, each adding its own table (DiT::make_cond, model.mm:317-347)
+    if (!s.tvec) return e.fail("dit: mod_table needs state->tvec");
+    if ((rc = make_cond(st, s.tvec, L.mod_table, L.n1, L.n2, D, s.mods, e))) return rc;
   }
   const float* m = s.mods;
   // attention half

@@ -28,7 +28,10 @@ _TORCH_DT = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16, torch
 
 # C-ABI symbols declared in include/kh.h (checked by tests/test_abi.py)
 SYMBOLS = ["kh_version", "kh_gemm", "kh_attention", "kh_rms_norm", "kh_qk_norm_rope", "kh_gemv", "kh_make_cond",
-           "kh_gemm_f32", "kh_rope_tables", "kh_dit_layer_forward", "kh_dit_forward"]
+           "kh_gemm_f32", "kh_rope_tables", "kh_dit_layer_forward", "kh_dit_forward",
+           "kh_qw_open", "kh_qw_close", "kh_qw_count", "kh_qw_version", "kh_qw_meta", "kh_qw_at", "kh_qw_find",
+           "kh_qw_upload", "kh_stream_create", "kh_stream_destroy", "kh_stream_sync", "kh_alloc", "kh_free",
+           "kh_upload", "kh_download"]
 
 
 class KhError(RuntimeError):
@@ -91,8 +94,16 @@ def load():
                                              ctypes.POINTER(DitStateC), i, cp, i]
         lib.kh_dit_forward.argtypes = [vp, ctypes.POINTER(DitConfig), ctypes.POINTER(DitLayerC), i,
                                        ctypes.POINTER(DitStateC), i, cp, i]
-        for name in SYMBOLS[2:]:
+        for name in SYMBOLS[2:11]:
             getattr(lib, name).restype = i
+        sz = ctypes.c_size_t
+        lib.kh_stream_create.argtypes, lib.kh_stream_create.restype = [ctypes.POINTER(vp), cp, i], i
+        lib.kh_stream_destroy.argtypes, lib.kh_stream_destroy.restype = [vp], i
+        lib.kh_stream_sync.argtypes, lib.kh_stream_sync.restype = [vp, cp, i], i
+        lib.kh_alloc.argtypes, lib.kh_alloc.restype = [ctypes.POINTER(vp), sz, cp, i], i
+        lib.kh_free.argtypes, lib.kh_free.restype = [vp], i
+        lib.kh_upload.argtypes = lib.kh_download.argtypes = [vp, vp, vp, sz, cp, i]
+        lib.kh_upload.restype = lib.kh_download.restype = i
         _lib = lib
     return _lib
 

@@ -1,0 +1,113 @@
+"""A reference-architecture DiT loaded from a packed .qw file (tools/convert.py:174-224 layout: int8 weights with
+f32 group-128 scales, fused q|k|v|gate, interleaved SwiGLU gate/up, per-layer mod tables, a high-gain q.k
+dimension carried in fp32) and run through kh_qw_upload + kh_dit_forward, against the oracle's composition of
+DiT::forward (engine/src/model.mm:317-385, 512-538) on the same file. Tolerance: <= 1.6 % relative L2 of the
+velocity (README.md:121's per-forward budget). Also the runtime surface (streams, alloc, copies)."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.helpers import rel_l2
+
+pytestmark = pytest.mark.gpu
+TOL = 1.6e-2
+
+
+def oracle_forward(f, shape, big, txt, z, t, tvec, cos, sin):
+    D, kvD, T = shape.dim, shape.kv_heads * 128, txt.shape[0]
+    dt, eps = O.BF16, shape.eps
+
+    def w(n):
+        return f.array(n), O.I8, f.array(n + ".s"), O.F32, 128
+
+    x = np.concatenate([txt, z @ f.array("first.w") + f.array("first.b")]).astype(np.float32)
+    for i in range(shape.layers):
+        p = f"L{i}."
+        m = O.make_cond(tvec, f.array(p + "mod").reshape(-1), f.array(p + "n1"), f.array(p + "n2"))
+        h = O.rms_norm(x, m[0], m[1], dt, eps, 0)
+        qkv = O.gemm(0, h, dt, *w(p + "qkvg"))
+        qkv, qb, kb = O.qk_norm_rope(qkv, dt, f.array(p + "qn"), f.array(p + "kn"), cos, sin, 0, shape.heads, D,
+                                     shape.kv_heads, eps, 0, big[i])
+        Q, K = np.ascontiguousarray(qkv[:, :D]), np.ascontiguousarray(qkv[:, D:D + kvD])
+        V, G = np.ascontiguousarray(qkv[:, D + kvD:D + 2 * kvD]), np.ascontiguousarray(qkv[:, D + 2 * kvD:])
+        ao = O.attention(Q, K, V, dt, shape.heads, shape.heads // shape.kv_heads, G=G,
+                         QB=qb if big[i] >= 0 else None, KB=kb if big[i] >= 0 else None)
+        O.gemm(O.EPI["resid_gate"], ao, dt, *w(p + "o"), C=x, vec=m[2])
+        h = O.rms_norm(x, m[3], m[4], dt, eps, 0)
+        mid = O.gemm(O.EPI["swiglu"], h, dt, *w(p + "gu"))
+        O.gemm(O.EPI["resid_gate"], mid, dt, *w(p + "down"), C=x, vec=m[5])
+    ln, lm = f.array("last.n"), f.array("last.mod")
+    hf = O.rms_norm(np.ascontiguousarray(x[T:]), ln * (1.0 + t + lm[0]), t + lm[1], O.F32, eps, 0)
+    return hf.astype(np.float64) @ f.array("last.w") + f.array("last.b")
+
+
+@pytest.mark.parametrize("big_gain", [None, (1, 5, 20.0)])
+def test_qw_dit_forward_matches_oracle(dev, tmp_path, big_gain):
+    from krea_image_amd import dit, qw
+    path = str(tmp_path / "dit_q8.qw")
+    qw.write_random_dit(path, D=256, kv_heads=1, FF=512, layers=2, quant=True, seed=11, big_gain=big_gain)
+    print(f"[qw dit] D=256 heads=2/1 ff=512 layers=2 big_gain={big_gain}", flush=True)
+    with qw.QwFile(path) as f:
+        f.upload()
+        run = dit.QwDit(f, 16, 8, 10, dev)
+        big = [L.big_dim for L in run.layers]
+        assert big == ([-1, -1] if big_gain is None else [-1, 5])
+        rng = np.random.default_rng(2)
+        txt = rng.standard_normal((16, 256)).astype(np.float32)
+        z = rng.standard_normal((80, 64)).astype(np.float32)
+        t = (0.5 * rng.standard_normal(256)).astype(np.float32)
+        tvec = (0.2 * rng.standard_normal(6 * 256)).astype(np.float32)
+        run.set_cond(t, tvec)
+        vel = torch.empty(80, 64, device=dev)
+        run.forward(torch.from_numpy(txt).to(dev), torch.from_numpy(z).to(dev), vel)
+        torch.cuda.synchronize()
+        got = vel.cpu().numpy()
+        ref = oracle_forward(f, run.shape, big, txt, z, t, tvec, run.cos.cpu().numpy(), run.sin.cpu().numpy())
+        err = rel_l2(got, ref)
+        print(f"    velocity rel_l2={err:.3e}", flush=True)
+        assert np.isfinite(got).all() and err <= TOL
+
+
+def test_qw_upload_places_every_tensor(dev, tmp_path):
+    from krea_image_amd import kh, qw
+    path = str(tmp_path / "w.qw")
+    rng = np.random.default_rng(5)
+    tensors = [("a", "f32", rng.standard_normal((300, 7)).astype(np.float32)),
+               ("b", "i8", rng.integers(-127, 128, (70000,), dtype=np.int8)),
+               ("c", "bf16", rng.standard_normal(999).astype(np.float32))]
+    qw.write_qw(path, tensors)
+    lib = kh.load()
+    with qw.QwFile(path) as f:
+        f.upload()
+        f.upload()  # idempotent
+        for name, _, _ in tensors:
+            ti = f.info(name)
+            host = f.array(name)
+            back = np.empty_like(host)
+            err = ctypes.create_string_buffer(256)
+            rc = lib.kh_download(None, back.ctypes.data, ti.dev, ti.nbytes, err, 256)
+            assert rc == 0, err.value
+            np.testing.assert_array_equal(back, host)
+
+
+def test_runtime_stream_alloc_copy(dev):
+    from krea_image_amd import kh
+    lib = kh.load()
+    err = ctypes.create_string_buffer(256)
+    s = ctypes.c_void_p()
+    assert lib.kh_stream_create(ctypes.byref(s), err, 256) == 0, err.value
+    p = ctypes.c_void_p()
+    n = 1 << 20
+    assert lib.kh_alloc(ctypes.byref(p), n, err, 256) == 0, err.value
+    src = np.random.default_rng(1).integers(0, 255, n, dtype=np.uint8)
+    dst = np.zeros(n, np.uint8)
+    assert lib.kh_upload(s, p, src.ctypes.data, n, err, 256) == 0, err.value
+    assert lib.kh_download(s, dst.ctypes.data, p, n, err, 256) == 0, err.value
+    np.testing.assert_array_equal(src, dst)
+    assert lib.kh_stream_sync(s, err, 256) == 0
+    assert lib.kh_free(p) == 0
+    assert lib.kh_stream_destroy(s) == 0
+    assert lib.kh_upload(None, None, src.ctypes.data, 16, err, 256) == -1 and b"null" in err.value
