@@ -56,16 +56,6 @@ __device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, const f
                                                   0);
 }
 
-// two f32 -> packed 16-bit (round to nearest even)
-template <int DT>
-__device__ __forceinline__ uint32_t pack16(float a, float b) {
-  if constexpr (DT == KH_BF16) {
-    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
-    return __builtin_bit_cast(uint32_t, (bf2){(__bf16)a, (__bf16)b});  // v_cvt_pk_bf16_f32
-  } else {
-    return (uint32_t)to16<DT>(a) | ((uint32_t)to16<DT>(b) << 16);
-  }
-}
 // acc + lo + hi of a packed 16-bit pair (v_dot2c_f32_{f16,bf16} against (1, 1))
 template <int DT>
 __device__ __forceinline__ float dot2_ones(uint32_t pr, float acc) {
@@ -264,8 +254,8 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
 #pragma unroll
         for (int e = 0; e < 4; e++) v[e] *= sigmoid_fast(from16<DT>((uint16_t)(gv[e >> 1] >> (16 * (e & 1)))));
       }
-      *(u32x2*)(op + d) = (u32x2){(uint32_t)to16<DT>(v[0]) | ((uint32_t)to16<DT>(v[1]) << 16),
-                                  (uint32_t)to16<DT>(v[2]) | ((uint32_t)to16<DT>(v[3]) << 16)};
+      *(u32x2*)(op + d) = (u32x2){pack16<DT>(v[0], v[1]),
+                                  pack16<DT>(v[2], v[3])};
     }
 }
 

@@ -17,10 +17,7 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // ---- 16-bit conversions (round to nearest even, as the reference's bf16(x) / half(x)) ----
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __builtin_bit_cast(uint32_t, f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  return __builtin_bit_cast(uint16_t, (__bf16)f);  // v_cvt_pk_bf16_f32: RNE, NaN stays NaN
 }
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
   return __builtin_bit_cast(uint16_t, (_Float16)f);  // v_cvt_f16_f32: RNE under the default mode
@@ -28,6 +25,16 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
 template <int DT>
 __device__ __forceinline__ uint16_t to16(float f) {
   return DT == KH_BF16 ? f32_to_bf16_bits(f) : f32_to_f16_bits(f);
+}
+// two f32 -> one dword of 16-bit values (a in the low half), round to nearest even; one instruction each
+template <int DT>
+__device__ __forceinline__ uint32_t pack16(float a, float b) {
+  if constexpr (DT == KH_BF16) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, (bf2){(__bf16)a, (__bf16)b});  // v_cvt_pk_bf16_f32
+  } else {
+    return __builtin_bit_cast(uint32_t, (f16x2){(_Float16)a, (_Float16)b});  // v_cvt_pk_f16_f32 / 2 cvt
+  }
 }
 template <int DT>
 __device__ __forceinline__ float from16(uint16_t h) {

@@ -44,7 +44,9 @@ constexpr int STAGE = BM * BK * 2;  // bytes of one 16-bit 256 x 64 tile
 constexpr int X_STAGES = 3, W_STAGES = 2;
 constexpr int GROUP_M = 8;
 
-enum { WF_16 = 0, WF_I8_CHANNEL = 1, WF_I8_GROUP = 2 };
+// weight formats; the group formats carry their scale type in the kernel so the K loop has no branches
+enum { WF_16 = 0, WF_I8_CHANNEL = 1, WF_I8_GROUP = 2, WF_I8_GROUP_F16 = 3, WF_I8_GROUP_BF16 = 4 };
+constexpr bool is_group(int wf) { return wf >= WF_I8_GROUP; }
 
 struct GemmArgs {
   const void* A;
@@ -52,7 +54,7 @@ struct GemmArgs {
   const void* S;
   void* C;
   const float* vec;
-  int M, N, K, lda, ldw, ldc, group, s_dtype;
+  int M, N, K, lda, ldw, ldc, gshift, s_dtype;
 };
 
 // 16-byte chunk XOR of LDS row `row` (rows are 128 bytes = 8 chunks of 8 k). Depends on row & 31 only, is a
@@ -86,15 +88,16 @@ struct WRaw<WF_16, KR> {
   u32x2 r[KR];
 };
 
-__device__ __forceinline__ float scale_from_bits(uint32_t b, int s_dtype) {
-  if (s_dtype == KH_F32) return __builtin_bit_cast(float, b);
-  if (s_dtype == KH_BF16) return __builtin_bit_cast(float, b << 16);
+template <int WF>
+__device__ __forceinline__ float scale_from_bits(uint32_t b) {
+  if constexpr (WF == WF_I8_GROUP) return __builtin_bit_cast(float, b);
+  if constexpr (WF == WF_I8_GROUP_BF16) return __builtin_bit_cast(float, b << 16);
   return (float)__builtin_bit_cast(_Float16, (uint16_t)b);
 }
 
 // Convert k-rows [8h, 8h+8) of column j to one 16-byte vector of 8 consecutive k (16-bit each).
 template <int ACT, int WF, int KR>
-__device__ __forceinline__ u32x4 convert_chunk(const WRaw<WF, KR>& w, int j, int h, int s_dtype) {
+__device__ __forceinline__ u32x4 convert_chunk(const WRaw<WF, KR>& w, int j, int h) {
   u32x4 out;
   if constexpr (WF == WF_16) {
     const uint32_t jj = (j & 1) * 2;
@@ -126,13 +129,13 @@ __device__ __forceinline__ u32x4 convert_chunk(const WRaw<WF, KR>& w, int j, int
     }
   } else {
     // group scales: round16(q * s) with the product rounded once in f32: fma(q + 128, s, -128 s)
-    const float s = scale_from_bits(w.s[j], s_dtype), nb = -128.0f * s;
+    const float s = scale_from_bits<WF>(w.s[j]), nb = -128.0f * s;
 #pragma unroll
     for (int p = 0; p < 4; p++) {
       const uint32_t a = w.r[8 * h + 2 * p] ^ 0x80808080u, b = w.r[8 * h + 2 * p + 1] ^ 0x80808080u;
       const float lo = __builtin_fmaf((float)((a >> (8 * j)) & 0xffu), s, nb);
       const float hi = __builtin_fmaf((float)((b >> (8 * j)) & 0xffu), s, nb);
-      out[p] = (uint32_t)to16<ACT>(lo) | ((uint32_t)to16<ACT>(hi) << 16);
+      out[p] = pack16<ACT>(lo, hi);
     }
   }
   return out;
@@ -206,9 +209,9 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
       else
         R.r[i] = vm_load_b32(src + i * wrow);
     }
-    if constexpr (WF == WF_I8_GROUP) {
-      const size_t g = (size_t)((t * BK) / p.group) * p.ldw + wcol;
-      if (p.s_dtype == KH_F32) {
+    if constexpr (is_group(WF)) {
+      const size_t g = (size_t)(t >> p.gshift) * p.ldw + wcol;
+      if constexpr (WF == WF_I8_GROUP) {
 #pragma unroll
         for (int j = 0; j < 4; j++) R.s[j] = vm_load_b32((const float*)p.S + g + j);
       } else {
@@ -223,7 +226,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NEWER));
 #pragma unroll
     for (int i = 0; i < KR; i++) vm_ready(R.r[i]);
-    if constexpr (WF == WF_I8_GROUP) {
+    if constexpr (is_group(WF)) {
 #pragma unroll
       for (int j = 0; j < 4; j++) vm_ready(R.s[j]);
     }
@@ -241,7 +244,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
     char* base = lds + (X_STAGES + stage) * STAGE;
 #pragma unroll
     for (int c = q * WCH / 4; c < (q + 1) * WCH / 4; c++)
-      *(u32x4*)(base + woff[c]) = convert_chunk<ACT, WF, KR>(R, c / H, c % H, p.s_dtype);
+      *(u32x4*)(base + woff[c]) = convert_chunk<ACT, WF, KR>(R, c / H, c % H);
   };
 
   // ---- MFMA operands: wave (wn, wm) owns n [128 wn, +128) x m [WME wm, +WME) = 4 x IB blocks of 32 x 32 ----
@@ -266,7 +269,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
   };
 
   const int nk = p.K / BK;
-  constexpr int LOADS = C_::LOADS + (WF == WF_I8_GROUP ? 4 : 0);
+  constexpr int LOADS = C_::LOADS + (is_group(WF) ? 4 : 0);
   using NewerT = std::integral_constant<int, LOADS>;
 
   // One K step: multiply stage t; convert raw(t + 1) into the other W stage between the MFMAs; the loads
@@ -380,8 +383,8 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
               else o[e] = v;
             }
             if constexpr (OUT16)
-              *(u32x2*)dst = (u32x2){(uint32_t)to16<ACT>(o[0]) | ((uint32_t)to16<ACT>(o[1]) << 16),
-                                     (uint32_t)to16<ACT>(o[2]) | ((uint32_t)to16<ACT>(o[3]) << 16)};
+              *(u32x2*)dst = (u32x2){pack16<ACT>(o[0], o[1]),
+                                     pack16<ACT>(o[2], o[3])};
             else
               *(f32x4*)dst = (f32x4){o[0], o[1], o[2], o[3]};
           }
@@ -440,7 +443,9 @@ template <int ACT>
 hipError_t launch_wf(int wf, int epi, const GemmArgs& a, hipStream_t st) {
   if (wf == WF_16) return launch_epi<ACT, WF_16>(epi, a, st);
   if (wf == WF_I8_CHANNEL) return launch_epi<ACT, WF_I8_CHANNEL>(epi, a, st);
-  return launch_epi<ACT, WF_I8_GROUP>(epi, a, st);
+  if (wf == WF_I8_GROUP) return launch_epi<ACT, WF_I8_GROUP>(epi, a, st);
+  if (wf == WF_I8_GROUP_F16) return launch_epi<ACT, WF_I8_GROUP_F16>(epi, a, st);
+  return launch_epi<ACT, WF_I8_GROUP_BF16>(epi, a, st);
 }
 
 }  // namespace
@@ -475,14 +480,17 @@ int gemm(hipStream_t st, int epi, const void* A, int a_dtype, const kh_weight& W
       wf = WF_I8_CHANNEL;
     } else {
       if (group % BK || K % group) return e.fail("gemm: int8 group %d must divide K and be a multiple of 64", group);
-      wf = WF_I8_GROUP;
+      if (group & (group - 1)) return e.fail("gemm: int8 group %d must be a power of two", group);
+      wf = W.s_dtype == KH_F32 ? WF_I8_GROUP : W.s_dtype == KH_F16 ? WF_I8_GROUP_F16 : WF_I8_GROUP_BF16;
     }
   } else {
     if (W.w_dtype != a_dtype) return e.fail("gemm: 16-bit weights must match the activation type");
     if (ldw % 8) return e.fail("gemm: ldw=%d must be a multiple of 8", ldw);
     wf = WF_16;
   }
-  GemmArgs a{A, W.w, W.s, C, (const float*)vec, M, N, K, lda, ldw, ldc, group, W.s_dtype};
+  int gshift = 0;  // log2(group / BK): K step t reads scale row t >> gshift
+  while ((BK << gshift) < group) gshift++;
+  GemmArgs a{A, W.w, W.s, C, (const float*)vec, M, N, K, lda, ldw, ldc, gshift, W.s_dtype};
   hipError_t r = a_dtype == KH_F16 ? launch_wf<KH_F16>(wf, epi, a, st) : launch_wf<KH_BF16>(wf, epi, a, st);
   if (r != hipSuccess) return e.hip(r, "gemm launch");
   return KH_OK;

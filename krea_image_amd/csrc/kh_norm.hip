@@ -74,8 +74,8 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__
       ((f32x4*)((float*)y + (size_t)row * ld_out))[c] = o;
     } else {
       ((u32x2*)((uint16_t*)y + (size_t)row * ld_out))[c] =
-          (u32x2){(uint32_t)to16<OUT>(o[0]) | ((uint32_t)to16<OUT>(o[1]) << 16),
-                  (uint32_t)to16<OUT>(o[2]) | ((uint32_t)to16<OUT>(o[3]) << 16)};
+          (u32x2){pack16<OUT>(o[0], o[1]),
+                  pack16<OUT>(o[2], o[3])};
     }
   }
 }
@@ -163,7 +163,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(uint16_t* __restrict_
   }
   u32x4 out;
 #pragma unroll
-  for (int i = 0; i < 4; i++) out[i] = (uint32_t)to16<DT>(o[2 * i]) | ((uint32_t)to16<DT>(o[2 * i + 1]) << 16);
+  for (int i = 0; i < 4; i++) out[i] = pack16<DT>(o[2 * i], o[2 * i + 1]);
   *(u32x4*)base = out;
 }
 
