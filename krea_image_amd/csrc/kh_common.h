@@ -95,6 +95,30 @@ __device__ __forceinline__ void vm_ready(T& r) {
   asm volatile("" : "+v"(r));
 }
 
+// Device-coherent 16-byte store / load (sc1: written through to / read from memory past L1 and L2, the
+// encoding of the memory model's agent-scope atomic accesses), for data exchanged between workgroups that
+// may run on different XCDs. Loads wait for themselves; stores are waited for by the caller.
+__device__ __forceinline__ void st_coherent_b128(float* p, f32x4 v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+}
+// eight device-coherent 16-byte loads at p + i * stride floats, completed before the statement ends
+__device__ __forceinline__ void ld_coherent_8x_b128(const float* p, int stride, f32x4 (&r)[8]) {
+  asm volatile(
+      "global_load_dwordx4 %0, %8, off sc1\n\t"
+      "global_load_dwordx4 %1, %9, off sc1\n\t"
+      "global_load_dwordx4 %2, %10, off sc1\n\t"
+      "global_load_dwordx4 %3, %11, off sc1\n\t"
+      "global_load_dwordx4 %4, %12, off sc1\n\t"
+      "global_load_dwordx4 %5, %13, off sc1\n\t"
+      "global_load_dwordx4 %6, %14, off sc1\n\t"
+      "global_load_dwordx4 %7, %15, off sc1\n\t"
+      "s_waitcnt vmcnt(0)"
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
+      : "v"(p), "v"(p + stride), "v"(p + 2 * stride), "v"(p + 3 * stride), "v"(p + 4 * stride),
+        "v"(p + 5 * stride), "v"(p + 6 * stride), "v"(p + 7 * stride)
+      : "memory");
+}
+
 // Workgroup barrier that is also a compiler memory barrier, without the release fence of __syncthreads
 // (which would also wait for LDS-direct loads still streaming in for later pipeline stages).
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }

@@ -26,7 +26,11 @@
 //  * Tile order: block ids are first made contiguous per XCD (the dispatcher deals workgroups round-robin
 //    to the 8 XCDs, each with its own L2), then walked in groups of 8 tile rows, so co-resident
 //    workgroups of one XCD share both X row panels and W column panels in that XCD's L2.
+#include <cstdlib>
+#include <map>
+#include <mutex>
 #include <type_traits>
+#include <utility>
 
 #include "kh_common.h"
 #include "kh_internal.h"
@@ -55,6 +59,9 @@ struct GemmArgs {
   void* C;
   const float* vec;
   int M, N, K, lda, ldw, ldc, gshift, s_dtype;
+  int sk_iters;  // stream-K: K steps per workgroup (0 = one tile per workgroup)
+  float* ws;     // stream-K partial tiles: 2 slots of BM x BN f32 per workgroup
+  int* cnt;      // stream-K arrival counts per tile (zero between launches)
 };
 
 // 16-byte chunk XOR of LDS row `row` (rows are 128 bytes = 8 chunks of 8 k). Depends on row & 31 only, is a
@@ -156,7 +163,7 @@ struct Cfg {
   static constexpr int LOADS = X_LOADS + KR;    // + 4 scale loads for the group format
 };
 
-template <int ACT, int WF, int EPI, int WAVES>
+template <int ACT, int WF, int EPI, int WAVES, bool SK>
 __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
   using C_ = Cfg<WAVES>;
   constexpr int NTHR = C_::NTHR, IB = C_::IB, X_LOADS = C_::X_LOADS, KR = C_::KR, WCH = C_::WCH;
@@ -166,16 +173,32 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
-  // ---- tile order (XCD-contiguous, then grouped by GROUP_M tile rows) ----
+  // ---- work of this workgroup: a range of K steps over the tile sequence. Data-parallel: one whole tile.
+  //      Stream-K (sk_iters > 0): sk_iters steps starting at (cta * sk_iters), crossing tile boundaries;
+  //      cta ids are made contiguous per XCD so one XCD's workgroups walk neighbouring tiles. ----
   const int tiles_n = (p.N + BN - 1) / BN, tiles_m = (p.M + BM - 1) / BM;
   const int total = tiles_n * tiles_m;
-  int pid = blockIdx.x;
-  if (total % 8 == 0) pid = (pid % 8) * (total / 8) + pid / 8;
+  const int nk = p.K / BK;
+  int cta = blockIdx.x, it, it_end;
+  if constexpr (SK) {
+    cta = (cta % 8) * (gridDim.x / 8) + cta / 8;  // host: gridDim.x % 8 == 0
+    it = cta * p.sk_iters;
+    it_end = min(it + p.sk_iters, total * nk);
+  } else {
+    if (total % 8 == 0) cta = (cta % 8) * (total / 8) + cta / 8;
+    it = cta * nk;
+    it_end = it + nk;
+  }
+  // tile index -> (m0, n0): walked in groups of GROUP_M tile rows so neighbouring tiles share panels in L2
   const int group_sz = GROUP_M * tiles_n;
-  const int first_m = (pid / group_sz) * GROUP_M;
-  const int gm = min(GROUP_M, tiles_m - first_m);
-  const int in_g = pid % group_sz;
-  const int m0 = (first_m + in_g % gm) * BM, n0 = (in_g / gm) * BN;
+  int m0 = 0, n0 = 0, kb = 0;  // current tile and its first K step
+  auto set_tile = [&](int tile) {
+    const int first_m = (tile / group_sz) * GROUP_M;
+    const int gm = min(GROUP_M, tiles_m - first_m);
+    const int in_g = tile % group_sz;
+    m0 = (first_m + in_g % gm) * BM;
+    n0 = (in_g / gm) * BN;
+  };
 
   // ---- X tile (activations) -> LDS directly: instruction r of wave w fills 1 KB block b = WAVES r + w,
   //      i.e. rows 8 WAVES r + 8w + lane/8; lane slot lane & 7 receives logical chunk (lane & 7) ^ swz(row)
@@ -183,25 +206,29 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
   const int xrow0 = wave * 8 + (lane >> 3);
   const int xchunk = ((lane & 7) ^ swz(xrow0)) * 8;
   int xoff[X_LOADS];
-#pragma unroll
-  for (int r = 0; r < X_LOADS; r++) xoff[r] = min(m0 + 8 * WAVES * r + xrow0, p.M - 1) * p.lda + xchunk;
   const uint16_t* xbase = (const uint16_t*)p.A;
   auto issue_x_to = [&](int t, int stage) {
     char* dst = lds + stage * STAGE + wave * 1024;
 #pragma unroll
     for (int r = 0; r < X_LOADS; r++)
-      __builtin_amdgcn_global_load_lds((const void*)(xbase + xoff[r] + t * BK), (lds_void*)(dst + r * WAVES * 1024),
-                                       16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(xbase + xoff[r] + (kb + t) * BK),
+                                       (lds_void*)(dst + r * WAVES * 1024), 16, 0, 0);
   };
 
   // ---- W tile: wave w loads k-rows [KR w, KR w + KR), lane columns n0 + 4 lane .. + 3 ----
-  const int wcol = min(n0 + lane * 4, p.N - 4);  // columns >= N (last tile) are never stored
   constexpr int WB = (WF == WF_16) ? 2 : 1;
-  const char* wbase = (const char*)p.W + ((size_t)(wave * KR) * p.ldw + wcol) * WB;
+  int wcol = 0;  // columns >= N (last tile) are loaded clamped and never stored
+  const char* wbase = nullptr;
   const size_t wrow = (size_t)p.ldw * WB;
+  auto set_operands = [&]() {
+#pragma unroll
+    for (int r = 0; r < X_LOADS; r++) xoff[r] = min(m0 + 8 * WAVES * r + xrow0, p.M - 1) * p.lda + xchunk;
+    wcol = min(n0 + lane * 4, p.N - 4);
+    wbase = (const char*)p.W + ((size_t)(wave * KR) * p.ldw + wcol) * WB;
+  };
   // untracked loads (see vm_load_b32): their waits are the explicit vmcnt of step() / the prologue
   auto issue_w = [&](int t, WRaw<WF, KR>& R) {
-    const char* src = wbase + (size_t)(t * BK) * wrow;
+    const char* src = wbase + (size_t)((kb + t) * BK) * wrow;
 #pragma unroll
     for (int i = 0; i < KR; i++) {
       if constexpr (WF == WF_16)
@@ -210,7 +237,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
         R.r[i] = vm_load_b32(src + i * wrow);
     }
     if constexpr (is_group(WF)) {
-      const size_t g = (size_t)(t >> p.gshift) * p.ldw + wcol;
+      const size_t g = (size_t)((kb + t) >> p.gshift) * p.ldw + wcol;
       if constexpr (WF == WF_I8_GROUP) {
 #pragma unroll
         for (int j = 0; j < 4; j++) R.s[j] = vm_load_b32((const float*)p.S + g + j);
@@ -256,10 +283,6 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
   for (int s = 0; s < 4; s++) sw[s] = (((2 * s + khalf) ^ swz(l32)) * 16);
 
   f32x16 acc[4][IB];
-#pragma unroll
-  for (int jb = 0; jb < 4; jb++)
-#pragma unroll
-    for (int ib = 0; ib < IB; ib++) acc[jb][ib] = (f32x16){};
 
   auto read_frags = [&](const char* xs, const char* ws, int s, u32x4 (&wf)[4], u32x4 (&xf)[IB]) {
 #pragma unroll
@@ -268,7 +291,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
     for (int ib = 0; ib < IB; ib++) xf[ib] = *(const u32x4*)(xs + x_rd + ib * 32 * 128 + sw[s]);
   };
 
-  const int nk = p.K / BK;
+  int ns = 0;  // K steps of the current segment
   constexpr int LOADS = C_::LOADS + (is_group(WF) ? 4 : 0);
   using NewerT = std::integral_constant<int, LOADS>;
 
@@ -277,7 +300,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
   // the same code: past the last step the loads re-fetch step nk - 1 into buffers nobody reads (stage
   // (t + 2) % 3 and the W stage of t + 1 are never the stage being multiplied), so the loop has no branches.
   auto step = [&](int t, WRaw<WF, KR>& Rc, WRaw<WF, KR>& Rl) {
-    const int tl = min(t + 2, nk - 1);
+    const int tl = min(t + 2, ns - 1);
     issue_x_to(tl, (t + 2) % X_STAGES);
     issue_w(tl, Rl);
     // step t + 1's loads (issued one step ago: its activations into LDS and raw(t + 1) = Rc) have landed
@@ -303,27 +326,103 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
     lds_barrier();  // this step's converted weights and (waited above) step t + 1's activations are visible
   };
 
+  bool first_seg = true;
+  if (it < it_end) for (;;) {  // segments; uniform: every thread walks the same ones (one when !SK)
+  const int tile = it / nk;
+  kb = it - tile * nk;
+  ns = min(nk - kb, it_end - it);
+  set_tile(tile);
+  set_operands();
+  if (SK && !first_seg) {
+    // the previous segment's epilogue stores and LDS reads are done before the pipeline restarts
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    lds_barrier();
+  }
+  first_seg = false;
+#pragma unroll
+  for (int jb = 0; jb < 4; jb++)
+#pragma unroll
+    for (int ib = 0; ib < IB; ib++) acc[jb][ib] = (f32x16){};
+
   WRaw<WF, KR> R0, R1;
   issue_x_to(0, 0);
   issue_w(0, R0);
-  issue_x_to(min(1, nk - 1), 1);
-  issue_w(min(1, nk - 1), R1);
+  issue_x_to(min(1, ns - 1), 1);
+  issue_w(min(1, ns - 1), R1);
   ready_w(R0, NewerT{});
 #pragma unroll
   for (int q = 0; q < 4; q++) store_w(R0, 0, q);
   lds_barrier();
   int t = 0;
-  for (; t + 1 < nk; t += 2) {
+  for (; t + 1 < ns; t += 2) {
     step(t, R1, R0);
     step(t + 1, R0, R1);
   }
-  if (t < nk) step(t, R1, R0);
+  if (t < ns) step(t, R1, R0);
   // The last steps' re-fetches must land before the LDS is reused below. The raw registers they target are
   // never read, so they are tied here, after the wait: otherwise the compiler would hand those registers to
   // other values while the (untracked) loads are still in flight and the loads would overwrite them.
   ready_w(R0, std::integral_constant<int, 0>{});
   ready_w(R1, std::integral_constant<int, 0>{});
   lds_barrier();
+
+  // ---- stream-K: a tile split over workgroups c0..c1 (K order). Each stores its partial accumulators to
+  //      its workspace slot and counts itself in; the last to arrive adds all partials in c0..c1 order
+  //      (deterministic whatever the arrival order) and runs the epilogue. No workgroup ever waits. ----
+  if (SK && ns != nk) {
+    const int c0 = (tile * nk) / p.sk_iters, c1 = (tile * nk + nk - 1) / p.sk_iters;
+    // a workgroup has at most two split tiles: slot 2c for its first tile, 2c + 1 for its last
+    auto slot = [&](int c) {
+      return p.ws + (size_t)(2 * c + (tile == (c * p.sk_iters) / nk ? 0 : 1)) * (BM * BN) + tid * 4;
+    };
+    // Partials and counts are exchanged device-coherently per access (sc1: through to memory, past both cache
+    // levels, as the agent-scope atomics of the memory model are), with no whole-cache write-back or
+    // invalidate: the workgroups of one tile may sit on different XCDs, whose L2s are not coherent.
+    {
+      float* mine = slot(cta);
+#pragma unroll
+      for (int jb = 0; jb < 4; jb++)
+#pragma unroll
+        for (int ib = 0; ib < IB; ib++)
+#pragma unroll
+          for (int g = 0; g < 4; g++)
+            st_coherent_b128(mine + (size_t)((jb * IB + ib) * 4 + g) * (NTHR * 4),
+                             (f32x4){acc[jb][ib][4 * g], acc[jb][ib][4 * g + 1], acc[jb][ib][4 * g + 2],
+                                     acc[jb][ib][4 * g + 3]});
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial has reached memory
+    lds_barrier();                                      // ... and every thread's
+    // the arrival count is broadcast through the (now idle) first LDS word; the epilogue writes there only
+    // after its own barrier, which every thread reaches after reading it
+    if (tid == 0)
+      *(volatile int*)lds = __hip_atomic_fetch_add(p.cnt + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    lds_barrier();
+    if (*(volatile int*)lds != c1 - c0) {
+      it += ns;
+      if (it >= it_end) break;
+      continue;  // another workgroup finishes this tile
+    }
+    // sum = p_c0 + p_c0+1 + ... in K order (own partial re-read like the others, so the association does
+    // not depend on which workgroup arrived last); 8 quads per batch of loads
+    static_assert(IB * 4 == 8, "fix-up batches assume 8 accumulator quads per jb");
+#pragma unroll
+    for (int jb = 0; jb < 4; jb++)
+#pragma unroll
+      for (int ib = 0; ib < IB; ib++) acc[jb][ib] = (f32x16){};
+    for (int c = c0; c <= c1; c++) {
+      const float* src = slot(c);
+#pragma unroll
+      for (int jb = 0; jb < 4; jb++) {
+        f32x4 v[8];
+        ld_coherent_8x_b128(src + (size_t)jb * 8 * (NTHR * 4), NTHR * 4, v);
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) acc[jb][u >> 2][4 * (u & 3) + e] += v[u][e];
+      }
+    }
+    if (tid == 0) __hip_atomic_store(p.cnt + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next launch
+  }
 
   // ---- epilogue. The LDS is free after the last barrier: the block's 256 column scales and vec entries
   //      are staged as f32, then the finished values are staged row-major and written out (or, for the
@@ -413,16 +512,22 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
     }
     if (pass + 1 < BM / PASS_ROWS) lds_barrier();
   }
+  if constexpr (!SK) break;
+  it += ns;
+  if (it >= it_end) break;
+  }  // segments
 }
 
 template <int ACT, int WF>
-hipError_t launch_epi(int epi, const GemmArgs& a, hipStream_t st) {
-  const int tiles = ((a.N + BN - 1) / BN) * ((a.M + BM - 1) / BM);
-  dim3 grid(tiles), block(64 * WAVES_DEFAULT);
+hipError_t launch_epi(int epi, const GemmArgs& a, int grid_x, hipStream_t st) {
+  dim3 grid(grid_x), block(64 * WAVES_DEFAULT);
   switch (epi) {
-#define KH_CASE(E)                                                        \
-  case E:                                                                 \
-    hipLaunchKernelGGL((gemm_kernel<ACT, WF, E, WAVES_DEFAULT>), grid, block, 0, st, a); \
+#define KH_CASE(E)                                                                          \
+  case E:                                                                                   \
+    if (a.sk_iters > 0)                                                                     \
+      hipLaunchKernelGGL((gemm_kernel<ACT, WF, E, WAVES_DEFAULT, true>), grid, block, 0, st, a);  \
+    else                                                                                    \
+      hipLaunchKernelGGL((gemm_kernel<ACT, WF, E, WAVES_DEFAULT, false>), grid, block, 0, st, a); \
     break;
     KH_CASE(KH_EPI_STORE16)
     KH_CASE(KH_EPI_F32)
@@ -440,12 +545,101 @@ hipError_t launch_epi(int epi, const GemmArgs& a, hipStream_t st) {
 }
 
 template <int ACT>
-hipError_t launch_wf(int wf, int epi, const GemmArgs& a, hipStream_t st) {
-  if (wf == WF_16) return launch_epi<ACT, WF_16>(epi, a, st);
-  if (wf == WF_I8_CHANNEL) return launch_epi<ACT, WF_I8_CHANNEL>(epi, a, st);
-  if (wf == WF_I8_GROUP) return launch_epi<ACT, WF_I8_GROUP>(epi, a, st);
-  if (wf == WF_I8_GROUP_F16) return launch_epi<ACT, WF_I8_GROUP_F16>(epi, a, st);
-  return launch_epi<ACT, WF_I8_GROUP_BF16>(epi, a, st);
+hipError_t launch_wf(int wf, int epi, const GemmArgs& a, int g, hipStream_t st) {
+  if (wf == WF_16) return launch_epi<ACT, WF_16>(epi, a, g, st);
+  if (wf == WF_I8_CHANNEL) return launch_epi<ACT, WF_I8_CHANNEL>(epi, a, g, st);
+  if (wf == WF_I8_GROUP) return launch_epi<ACT, WF_I8_GROUP>(epi, a, g, st);
+  if (wf == WF_I8_GROUP_F16) return launch_epi<ACT, WF_I8_GROUP_F16>(epi, a, g, st);
+  return launch_epi<ACT, WF_I8_GROUP_BF16>(epi, a, g, st);
+}
+
+// ---- stream-K workspace: per (device, stream), allocated on first use and kept until the process ends.
+//      Launches on one stream are ordered, so one workspace per stream is race-free. ----
+constexpr int SK_MAX_TILES = 1 << 16;
+constexpr int SK_MIN_ITERS = 4;  // below this many K steps per workgroup the partial traffic dominates
+
+struct SkWorkspace {
+  float* ws = nullptr;
+  int* cnt = nullptr;
+  int ctas = 0;
+};
+
+std::mutex sk_mu;
+std::map<std::pair<int, hipStream_t>, SkWorkspace> sk_map;
+std::map<int, int> sk_ctas;  // device -> workgroups of one full wave (one per CU), a multiple of 8
+
+// KH_GEMM_STREAMK=0 keeps every launch data-parallel (read per call, so a host can switch it at run time)
+bool sk_enabled() {
+  const char* e = getenv("KH_GEMM_STREAMK");
+  return !(e && e[0] == '0');
+}
+
+// workgroups for a stream-K launch on `dev` (0: unavailable)
+int sk_cta_count(int dev) {
+  std::lock_guard<std::mutex> lk(sk_mu);
+  auto it = sk_ctas.find(dev);
+  if (it != sk_ctas.end()) return it->second;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 0;
+  const int c = cus - cus % 8;
+  sk_ctas[dev] = c;
+  return c;
+}
+
+const SkWorkspace* sk_workspace(int dev, hipStream_t st, int ctas) {
+  std::lock_guard<std::mutex> lk(sk_mu);
+  auto key = std::make_pair(dev, st);
+  auto it = sk_map.find(key);
+  if (it != sk_map.end()) return it->second.ws ? &it->second : nullptr;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return nullptr;
+  SkWorkspace w;
+  w.ctas = ctas;
+  const size_t ws_bytes = (size_t)2 * ctas * BM * BN * sizeof(float);
+  if (hipMalloc((void**)&w.ws, ws_bytes) != hipSuccess) w.ws = nullptr;
+  if (w.ws && hipMalloc((void**)&w.cnt, SK_MAX_TILES * sizeof(int)) != hipSuccess) {
+    (void)hipFree(w.ws);
+    w.ws = nullptr;
+  }
+  if (w.ws && hipMemset(w.cnt, 0, SK_MAX_TILES * sizeof(int)) != hipSuccess) {
+    (void)hipFree(w.ws);
+    (void)hipFree(w.cnt);
+    w.ws = nullptr;
+  }
+  (void)hipGetLastError();  // a failed allocation leaves the data-parallel path in place, not an error
+  sk_map[key] = w;
+  return w.ws ? &sk_map[key] : nullptr;
+}
+
+// Data-parallel (one tile per workgroup) unless the tiles fill the last wave of workgroups poorly; then
+// stream-K spreads the tiles' K steps evenly over one wave of workgroups.
+void plan_launch(GemmArgs& a, hipStream_t st, int& grid_x) {
+  const int tiles = ((a.N + BN - 1) / BN) * ((a.M + BM - 1) / BM);
+  const int nk = a.K / BK;
+  grid_x = tiles;
+  a.sk_iters = 0;
+  a.ws = nullptr;
+  a.cnt = nullptr;
+  if (!sk_enabled() || tiles > SK_MAX_TILES) return;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return;
+  const int ctas = sk_cta_count(dev);
+  if (ctas <= 0) return;
+  // Stream-K staggers the workgroups' K offsets, so neighbouring tiles no longer share X / W panels in L2
+  // at the same time: measured, it loses to data-parallel launches that fill >= 75 % of their last wave
+  // (4608 x 3072 x 3072: 140 vs 103 us) and wins where most CUs would idle (1536 x 3072 x 12288: 156 vs
+  // 303 us). It is used below 60 % occupancy.
+  const int rounds = (tiles + ctas - 1) / ctas;
+  if ((double)tiles / ((double)rounds * ctas) >= 0.6) return;
+  const long long iters = (long long)tiles * nk;
+  const int per = (int)((iters + ctas - 1) / ctas);
+  if (per < SK_MIN_ITERS) return;
+  const SkWorkspace* w = sk_workspace(dev, st, ctas);
+  if (!w) return;
+  a.sk_iters = per;
+  a.ws = w->ws;
+  a.cnt = w->cnt;
+  grid_x = ctas;
 }
 
 }  // namespace
@@ -490,8 +684,11 @@ int gemm(hipStream_t st, int epi, const void* A, int a_dtype, const kh_weight& W
   }
   int gshift = 0;  // log2(group / BK): K step t reads scale row t >> gshift
   while ((BK << gshift) < group) gshift++;
-  GemmArgs a{A, W.w, W.s, C, (const float*)vec, M, N, K, lda, ldw, ldc, gshift, W.s_dtype};
-  hipError_t r = a_dtype == KH_F16 ? launch_wf<KH_F16>(wf, epi, a, st) : launch_wf<KH_BF16>(wf, epi, a, st);
+  GemmArgs a{A, W.w, W.s, C, (const float*)vec, M, N, K, lda, ldw, ldc, gshift, W.s_dtype, 0, nullptr, nullptr};
+  int grid_x = 0;
+  plan_launch(a, st, grid_x);
+  hipError_t r = a_dtype == KH_F16 ? launch_wf<KH_F16>(wf, epi, a, grid_x, st)
+                                   : launch_wf<KH_BF16>(wf, epi, a, grid_x, st);
   if (r != hipSuccess) return e.hip(r, "gemm launch");
   return KH_OK;
 }

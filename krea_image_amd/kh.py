@@ -142,12 +142,40 @@ class Weight:
                         F32 if self.s is None else dtype_code(self.s.dtype), self.group)
 
 
+_F32_OUT_EPI = (1, 2, 3, 7)  # F32, RESID_GATE, RESID, BIAS_F32
+
+
+def _bytes_after(t) -> int:
+    """Bytes of t's storage from t's first element to the end (what a raw-pointer kernel may touch)."""
+    if not isinstance(t, torch.Tensor):
+        return 1 << 62  # raw device addresses (uploaded weight files) are the caller's responsibility
+    st = t.untyped_storage()
+    return st.nbytes() - (t.data_ptr() - st.data_ptr())
+
+
+def _need(t, name: str, rows: int, cols: int, ld: int, esize: int):
+    need = ((rows - 1) * ld + cols) * esize if rows > 0 and cols > 0 else 0
+    if _bytes_after(t) < need:
+        raise KhError(f"gemm: {name} holds {_bytes_after(t)} bytes, the call addresses {need}")
+
+
 def gemm(epi, A: torch.Tensor, W: Weight, C: torch.Tensor, M: int, N: int, K: int, lda: int, ldw: int, ldc: int,
          vec: Optional[torch.Tensor] = None):
-    """krea::Metal::gemm (engine/src/metal.mm:146-163): acc = A[M,K] x Wt[K,N], then epilogue `epi`."""
+    """krea::Metal::gemm (engine/src/metal.mm:146-163): acc = A[M,K] x Wt[K,N], then epilogue `epi`.
+    Tensor arguments are checked on the host (dtype of C for the epilogue, storage covering every strided
+    row) so a mis-sized buffer raises instead of reaching the device."""
     lib = load()
     if isinstance(epi, str):
         epi = EPI[epi]
+    if isinstance(C, torch.Tensor) and isinstance(A, torch.Tensor):
+        want = torch.float32 if epi in _F32_OUT_EPI else A.dtype
+        if C.dtype != want:
+            raise KhError(f"gemm: epilogue {epi} writes {want}, C is {C.dtype}")
+        _need(A, "A", M, K, lda, A.element_size())
+        _need(C, "C", M, N // 2 if epi == EPI["swiglu"] else N, ldc, C.element_size())
+        _need(W.w, "W", K, N, ldw, 1 if W.w.dtype == torch.int8 else 2)
+        if vec is not None:
+            _need(vec, "vec", 1, N, N, 4)
     err = ctypes.create_string_buffer(512)
     wc = W.c()
     rc = lib.kh_gemm(_stream(), epi, _ptr(A), dtype_code(A.dtype), ctypes.byref(wc), _ptr(C), M, N, K, lda, ldw, ldc,

@@ -82,3 +82,24 @@ def test_gemm_rejects_bad_int8_group(lib):
     assert rc == -1 and "group" in err
     rc, err = _gemm_call(lib, w=kh._WeightC(16, 16, kh.BF16, kh.F32, 0))
     assert rc == -1 and "match the activation type" in err
+
+
+def test_gemm_front_end_rejects_wrong_output_dtype_and_short_buffers():
+    """kh.gemm checks torch arguments on the host before any launch (CPU tensors: nothing reaches a device)."""
+    import torch
+    from krea_image_amd import kh
+    A = torch.zeros(256, 128, dtype=torch.float16)
+    W = kh.Weight(torch.zeros(128, 64, dtype=torch.int8), torch.ones(64, dtype=torch.float16))
+    vec = torch.zeros(64)
+    with pytest.raises(kh.KhError, match="writes torch.float32"):
+        kh.gemm("resid_gate", A, W, torch.zeros(256, 64, dtype=torch.float16), 256, 64, 128, 128, 64, 64, vec)
+    with pytest.raises(kh.KhError, match="C holds"):
+        kh.gemm("resid", A, W, torch.zeros(255, 64), 256, 64, 128, 128, 64, 64)
+    with pytest.raises(kh.KhError, match="A holds"):
+        kh.gemm("store16", torch.zeros(100, 128, dtype=torch.float16), W, torch.zeros(256, 64, dtype=torch.float16),
+                256, 64, 128, 128, 64, 64)
+    with pytest.raises(kh.KhError, match="C holds"):  # a column view that runs past the end with ldc = 128
+        C = torch.zeros(256, 128, dtype=torch.float16)[:, 96:]
+        kh.gemm("store16", A, W, C, 256, 64, 128, 128, 64, 128)
+    with pytest.raises(kh.KhError, match="vec holds"):
+        kh.gemm("bias_f32", A, W, torch.zeros(256, 64), 256, 64, 128, 128, 64, 64, torch.zeros(32))
