@@ -9,7 +9,8 @@
  * launch error; `err` (if non-NULL) receives a NUL-terminated message of at most errlen bytes, the
  * convention of the reference's C ABI (engine/src/krea.h:57-73, engine/src/pipeline.mm:594-641).
  *
- * Ops are asynchronous on `stream` (a hipStream_t; NULL = the null stream) and never allocate.
+ * Ops are asynchronous on `stream` (a hipStream_t; NULL = the null stream). Ops do not allocate, with one
+ * exception: kh_gemm keeps a per-(device, stream) stream-K workspace (see kh_gemm).
  */
 #ifndef KH_H
 #define KH_H
@@ -59,8 +60,13 @@ typedef struct kh_weight {
 
 /* acc[M, N] = A[M, K] (a_dtype KH_F16 / KH_BF16, row stride lda) x Wt[K, N], fp32 accumulation, then
  * `epi`. vec: f32 [N] gate (RESID_GATE) or bias (BIAS16 / BIAS_F32), else unused. C row stride ldc in
- * elements of the output type. Constraints: M > 0, N % 64 == 0, K % 64 == 0, int8 group % 64 == 0,
- * 16-byte aligned A / W rows (lda % 8 == 0, ldw % 16 == 0 for int8, % 8 for 16-bit).
+ * elements of the output type. Constraints: M > 0, N % 64 == 0, K % 64 == 0, int8 group a power of two
+ * >= 64 dividing K, 16-byte aligned A / W rows (lda % 8 == 0, ldw % 16 == 0 for int8, % 8 for 16-bit).
+ * Shapes whose 256 x 256 tiles would fill under 60 % of a wave of workgroups run stream-K (the tiles' K
+ * steps spread over one workgroup per CU); those launches use a workspace of 2 x CUs x 256 KiB + 256 KiB
+ * that kh_gemm allocates once per (device, stream) on first need and keeps until the process ends (on a
+ * capturing stream without one, the launch stays data-parallel). Results are deterministic either way.
+ * KH_GEMM_STREAMK=0 in the environment keeps every launch data-parallel.
  * Replaces krea::Metal::gemm (engine/src/metal.h:66-69, engine/src/metal.mm:146-163). */
 int kh_gemm(kh_stream stream, int epi, const void* A, int a_dtype, const kh_weight* W, void* C, int M, int N, int K,
             int lda, int ldw, int ldc, const void* vec, char* err, int errlen);

@@ -19,10 +19,12 @@
 //    the contraction needs no data movement (the key order inside a step is irrelevant to the sum).
 //  * K tiles stream global -> LDS directly (16-byte DMA per lane), rows of 256 B with the 16-byte chunk
 //    XOR-swizzled by (row & 15). V tiles are transposed on the way in (4 keys x 8 dims per thread,
-//    v_perm_b32 into 8 dims x 4 keys) into V^T rows of 128 B, chunk XOR (d & 7) ^ (d >> 3 & 7).
+//    v_perm_b32 into 8 dims x 4 keys) into V^T rows of 128 B (key order and swizzle: vt_off).
 //  * 4 waves x 32 queries per workgroup, 64-key blocks double-buffered (2 x 32 KB); two workgroups per CU.
 //  * Lazy online softmax (the reference's LAZY_TH idea, attention.metal:33-37): the running max only moves
 //    when a block's max exceeds it by more than 8 (log2 units), so most blocks skip the O rescale.
+#include <type_traits>
+
 #include "kh_common.h"
 #include "kh_internal.h"
 
@@ -67,7 +69,15 @@ __device__ __forceinline__ float dot2_ones(uint32_t pr, float acc) {
   }
 }
 
-__device__ __forceinline__ int vt_chunk(int d, int kc) { return kc ^ (d & 7) ^ ((d >> 3) & 7); }
+// V^T row d is 128 B = 8 chunks of 16 B = 16 quads of 4 keys. Key quad kq goes to chunk
+// 2 (kq >> 2) + (kq & 1), half (kq >> 1) & 1, so the two quads one MFMA lane needs in key step j
+// (4 j + hh and 4 j + 2 + hh) are one 16-byte chunk, 2 j + hh: one ds_read_b128 per operand, already in
+// operand order. Chunks are XOR-swizzled by ((d >> 1) ^ (d >> 4)) & 7. LDS serves 16 lanes per cycle for
+// 16-byte reads and 32 for 8-byte writes (64 banks x 4 B); with the store order of store_vt, both the
+// operand reads (16 consecutive rows, one logical chunk) and the transpose writes hit 64 distinct banks.
+__device__ __forceinline__ int vt_off(int d, int kq) {
+  return d * 128 + (((2 * (kq >> 2) + (kq & 1)) ^ (((d >> 1) ^ (d >> 4)) & 7)) * 16) + ((kq >> 1) & 1) * 8;
+}
 
 template <int DT, bool GATE, bool BIG, bool CAUSAL>
 __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
@@ -109,8 +119,11 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
                                        (lds_void*)(lds + buf * BUF + (4 * r + wave) * 1024), 16, 0, 0);
     }
   };
-  // ---- V tile: thread -> keys 4 kq .. 4 kq + 3 (kq = tid / 16), dims 8 c .. 8 c + 7 (c = tid & 15) ----
-  const int vkq = tid >> 4, vc = tid & 15;
+  // ---- V tile: thread -> keys 4 vkq .. 4 vkq + 3, dims 8 vc .. 8 vc + 7. Within a wave the four 16-lane
+  //      groups take key quads 4w + {0, 2, 1, 3}, so each half wave writes quads of both 8-byte halves of
+  //      a chunk (see vt_off) ----
+  const int vlane = tid & 63;
+  const int vkq = 4 * wave + (((vlane >> 4) & 1) << 1 | ((vlane >> 5) & 1)), vc = vlane & 15;
   const uint16_t* vbase = (const uint16_t*)p.V + kvh * D + vc * 8;
   u32x4 vr[4];
   auto load_v = [&](int b) {
@@ -120,17 +133,20 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
       vr[r] = *(const u32x4*)(vbase + (size_t)key * p.ldv);
     }
   };
-  auto store_vt = [&](int buf) {  // 8 dims x 4 keys: V^T[d][4 kq .. 4 kq + 3] as one 8-byte write per d
+  // 8 dims x 4 keys: V^T[d][4 vkq .. 4 vkq + 3] as one 8-byte write per d. Write i covers dim
+  // 8 vc + (i ^ (vc & 1)): odd-vc lanes swap the two dims of each dword, which only changes the v_perm
+  // selector, and spreads the half wave's writes over both row parities.
+  const uint32_t sel_lo = (vc & 1) ? 0x07060302u : 0x05040100u, sel_hi = (vc & 1) ? 0x05040100u : 0x07060302u;
+  auto store_vt = [&](int buf) {
     char* vt = lds + buf * BUF + KT_BYTES;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-      const int d = vc * 8 + i;
+      const int d = vc * 8 + (i ^ (vc & 1));
       const int w = i >> 1;  // dword of the 16-byte row chunk holding dims 2w, 2w + 1
-      const uint32_t sel = (i & 1) ? 0x07060302u : 0x05040100u;
-      const uint32_t lo = __builtin_amdgcn_perm(vr[1][w], vr[0][w], sel);  // keys 4kq, 4kq+1 of dim d
-      const uint32_t hi = __builtin_amdgcn_perm(vr[3][w], vr[2][w], sel);  // keys 4kq+2, 4kq+3
-      const int kc = vkq >> 1;  // 16-byte chunk (8 keys) of the V^T row
-      *(u32x2*)(vt + d * 128 + vt_chunk(d, kc) * 16 + (vkq & 1) * 8) = (u32x2){lo, hi};
+      const uint32_t sel = (i & 1) ? sel_hi : sel_lo;
+      const uint32_t lo = __builtin_amdgcn_perm(vr[1][w], vr[0][w], sel);  // keys 4vkq, 4vkq+1 of dim d
+      const uint32_t hi = __builtin_amdgcn_perm(vr[3][w], vr[2][w], sel);  // keys 4vkq+2, 4vkq+3
+      *(u32x2*)(vt + vt_off(d, vkq)) = (u32x2){lo, hi};
     }
   };
   auto stage_kb = [&](int b, int buf) {
@@ -150,7 +166,10 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
     lds_barrier();
   }
-  for (int b = 0; b < nblk; b++) {
+  // One 64-key block. MASK: the block holds keys >= Lk or (causal) keys above some query's diagonal; only
+  // then are scores masked, so full blocks carry no per-score compares or selects.
+  auto process = [&](int b, auto mask_c) {
+    constexpr bool MASK = decltype(mask_c)::value;
     const int cur = b & 1;
     const bool has_next = b + 1 < nblk;
     if (has_next) {
@@ -175,27 +194,26 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
     }
 
     // block max on the raw scores (the positive scale commutes with max); masked scores are -inf
-    const int key0 = b * BKEYS;
-    const bool need_mask = CAUSAL || (key0 + BKEYS > p.Lk);
     float bmax = -INFINITY;
 #pragma unroll
     for (int kh = 0; kh < 2; kh++)
 #pragma unroll
       for (int i = 0; i < 16; i++) {
-        const int kl = kh * 32 + (i >> 2) * 8 + hh * 4 + (i & 3);
         float s = st[kh][i];
-        if (BIG) s += qb * kb_s[cur][kl];
-        if (need_mask) {
-          const int key = key0 + kl;
+        if constexpr (BIG) s += qb * kb_s[cur][kh * 32 + (i >> 2) * 8 + hh * 4 + (i & 3)];
+        if constexpr (MASK) {
+          const int key = b * BKEYS + kh * 32 + (i >> 2) * 8 + hh * 4 + (i & 3);
           if (key >= p.Lk || (CAUSAL && key > q + p.q_pos0)) s = -INFINITY;
         }
         st[kh][i] = s;
         bmax = fmaxf(bmax, s);
       }
     bmax = fmaxf(bmax, __shfl_xor(bmax, 32)) * p.scale_log2;
-    // lazy max update (log2 units): only when some query of the wave grew by more than LAZY_TH
-    if (__any(bmax > m + LAZY_TH)) {
+    // lazy max update (log2 units): only when some query of the wave grew by more than LAZY_TH; the
+    // condition is wave-uniform and read into a scalar so the rescale stays a branch, not 64 selects
+    if (__builtin_amdgcn_readfirstlane(__any(bmax > m + LAZY_TH))) {
       const float m_new = fmaxf(m, bmax);
+      asm volatile("" ::: "memory");  // not speculated: the compiler would otherwise multiply by 1 always
       const float alpha = __builtin_amdgcn_exp2f(m - m_new);
       m = m_new;
       l *= alpha;
@@ -221,10 +239,9 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
       const int d = db * 32 + l32;
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        const int k0 = 16 * j + 4 * hh, k1 = k0 + 8;  // keys of operand slots 0..3 and 4..7
-        const u32x2 a = *(const u32x2*)(vt + d * 128 + vt_chunk(d, k0 >> 3) * 16 + (k0 & 7) * 2);
-        const u32x2 c = *(const u32x2*)(vt + d * 128 + vt_chunk(d, k1 >> 3) * 16 + (k1 & 7) * 2);
-        o[db] = mfma32<DT>((u32x4){a[0], a[1], c[0], c[1]}, pf[j], o[db]);
+        // operand slots 0..3: key quad 4 j + hh, slots 4..7: quad 4 j + 2 + hh (one chunk, see vt_off)
+        const u32x4 vf = *(const u32x4*)(vt + vt_off(d, 4 * j + hh));
+        o[db] = mfma32<DT>(vf, pf[j], o[db]);
       }
     }
 
@@ -233,7 +250,14 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
       __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));  // vmcnt(0): the next K tile has landed
     }
     lds_barrier();
-  }
+  };
+  // blocks [0, nfull) need no mask: all their keys are < Lk and (causal) <= the workgroup's first query
+  int nfull = p.Lk / BKEYS;
+  if (CAUSAL) nfull = min(nfull, max(0, (qblk + p.q_pos0 + 1) / BKEYS));
+  nfull = min(nfull, nblk);
+  int b = 0;
+  for (; b < nfull; b++) process(b, std::false_type{});
+  for (; b < nblk; b++) process(b, std::true_type{});
 
   // ---- normalise, gate, store: lane holds d = 32 db + 8 g + 4 hh + e of query q ----
   l += __shfl_xor(l, 32);
