@@ -20,7 +20,9 @@
 //  * K tiles stream global -> LDS directly (16-byte DMA per lane), rows of 256 B with the 16-byte chunk
 //    XOR-swizzled by (row & 15). V tiles are transposed on the way in (4 keys x 8 dims per thread,
 //    v_perm_b32 into 8 dims x 4 keys) into V^T rows of 128 B (key order and swizzle: vt_off).
-//  * 4 waves x 32 queries per workgroup, 64-key blocks double-buffered (2 x 32 KB); two workgroups per CU.
+//  * 4 waves x 32 queries per workgroup, 64-key blocks; K tiles double-buffered, V^T tiles triple-buffered
+//    (80 KB, two workgroups per CU). Software pipeline: block b issues S(b), then P V of block b - 1, and
+//    the softmax of block b runs on the VALU while those MFMAs execute.
 //  * Lazy online softmax (the reference's LAZY_TH idea, attention.metal:33-37): the running max only moves
 //    when a block's max exceeds it by more than 8 (log2 units), so most blocks skip the O rescale.
 #include <type_traits>
@@ -35,7 +37,8 @@ namespace {
 constexpr int D = 128, BQ = 128, BKEYS = 64, NTHR = 256;
 constexpr int KT_BYTES = BKEYS * D * 2;   // K tile: 64 rows x 256 B
 constexpr int VT_BYTES = D * BKEYS * 2;   // V^T tile: 128 rows x 128 B
-constexpr int BUF = KT_BYTES + VT_BYTES;  // one pipeline stage
+constexpr int K_STAGES = 2, V_STAGES = 3;  // V^T lives one block longer: P V of block b - 1 runs in block b
+constexpr int LDS_BYTES = K_STAGES * KT_BYTES + V_STAGES * VT_BYTES;  // 80 KB: two workgroups per CU
 constexpr float LAZY_TH = 8.0f;
 constexpr float M_INIT = -1.0e30f;        // finite: a fully masked block leaves exp2(-inf - M_INIT) = 0
 
@@ -81,14 +84,21 @@ __device__ __forceinline__ int vt_off(int d, int kq) {
 
 template <int DT, bool GATE, bool BIG, bool CAUSAL>
 __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
-  __shared__ __attribute__((aligned(1024))) char lds[2 * BUF];
-  __shared__ float kb_s[2][BKEYS];  // fp32 rank-1 key term of the staged block (BIG)
+  // [K stage 0 | K stage 1 | V^T stage 0 | 1 | 2] (+ the fp32 rank-1 key terms of two blocks when BIG)
+  __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES + (BIG ? 2 * BKEYS * 4 : 0)];
+  float* const kb_s = (float*)(lds + LDS_BYTES);  // [2][BKEYS], BIG only
   typedef __attribute__((address_space(3))) void lds_void;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hh = lane >> 5;
-  const int h = blockIdx.y, kvh = h / p.group;
-  const int qblk = blockIdx.x * BQ;
+  // Workgroup -> (head, query block). The dispatcher deals workgroups round-robin to the 8 XCDs (each
+  // with its own L2); ids are remapped so that each XCD walks whole heads in order: its resident
+  // workgroups then share one or two heads' K / V (2.4 MB per head at 4608 keys) in their L2.
+  const int nqb = (p.Lq + BQ - 1) / BQ, total = nqb * p.heads;
+  int wg = blockIdx.x;
+  if (total % 8 == 0) wg = (wg % 8) * (total / 8) + wg / 8;
+  const int h = wg / nqb, kvh = h / p.group;
+  const int qblk = (wg % nqb) * BQ;
   const int q = qblk + wave * 32 + l32;       // this lane's query
   const int qc = min(q, p.Lq - 1);            // clamped (rows >= Lq are computed, never stored)
 
@@ -116,7 +126,7 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
       const int key = min(b * BKEYS + row, p.Lk - 1);
       const int c = (lane & 15) ^ (row & 15);
       __builtin_amdgcn_global_load_lds((const void*)(kbase + (size_t)key * p.ldk + c * 8),
-                                       (lds_void*)(lds + buf * BUF + (4 * r + wave) * 1024), 16, 0, 0);
+                                       (lds_void*)(lds + buf * KT_BYTES + (4 * r + wave) * 1024), 16, 0, 0);
     }
   };
   // ---- V tile: thread -> keys 4 vkq .. 4 vkq + 3, dims 8 vc .. 8 vc + 7. Within a wave the four 16-lane
@@ -138,7 +148,7 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
   // selector, and spreads the half wave's writes over both row parities.
   const uint32_t sel_lo = (vc & 1) ? 0x07060302u : 0x05040100u, sel_hi = (vc & 1) ? 0x05040100u : 0x07060302u;
   auto store_vt = [&](int buf) {
-    char* vt = lds + buf * BUF + KT_BYTES;
+    char* vt = lds + K_STAGES * KT_BYTES + buf * VT_BYTES;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       const int d = vc * 8 + (i ^ (vc & 1));
@@ -150,13 +160,28 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
     }
   };
   auto stage_kb = [&](int b, int buf) {
-    if (BIG && tid < BKEYS) kb_s[buf][tid] = p.KB[(size_t)min(b * BKEYS + tid, p.Lk - 1) * p.ldkb + kvh];
+    if (BIG && tid < BKEYS) kb_s[buf * BKEYS + tid] = p.KB[(size_t)min(b * BKEYS + tid, p.Lk - 1) * p.ldkb + kvh];
   };
 
   f32x16 o[4];
 #pragma unroll
   for (int db = 0; db < 4; db++) o[db] = (f32x16){};
   float m = M_INIT, l = 0.f;
+
+  // O^T += V^T P^T of one block: P^T from registers, V^T from its LDS stage
+  auto pv = [&](const u32x4 (&pf)[4], int vbuf) {
+    const char* vt = lds + K_STAGES * KT_BYTES + vbuf * VT_BYTES;
+#pragma unroll
+    for (int db = 0; db < 4; db++) {
+      const int d = db * 32 + l32;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        // operand slots 0..3: key quad 4 j + hh, slots 4..7: quad 4 j + 2 + hh (one chunk, see vt_off)
+        const u32x4 vf = *(const u32x4*)(vt + vt_off(d, 4 * j + hh));
+        o[db] = mfma32<DT>(vf, pf[j], o[db]);
+      }
+    }
+  };
 
   if (nblk > 0) {
     issue_k(0, 0);
@@ -166,19 +191,20 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
     lds_barrier();
   }
-  // One 64-key block. MASK: the block holds keys >= Lk or (causal) keys above some query's diagonal; only
-  // then are scores masked, so full blocks carry no per-score compares or selects.
+  // Software pipeline over 64-key blocks: block b issues S(b) = K Q^T, then P V of block b - 1 (its P^T
+  // kept in registers, its V^T in the third LDS stage), then the softmax of S(b) runs on the VALU while
+  // those MFMAs execute. MASK: the block holds keys >= Lk or (causal) keys above some query's diagonal;
+  // only then are scores masked, so full blocks carry no per-score compares or selects.
+  u32x4 pf[4];  // P^T of the previous block
   auto process = [&](int b, auto mask_c) {
     constexpr bool MASK = decltype(mask_c)::value;
-    const int cur = b & 1;
     const bool has_next = b + 1 < nblk;
     if (has_next) {
-      issue_k(b + 1, cur ^ 1);
+      issue_k(b + 1, (b + 1) & 1);
       load_v(b + 1);
-      stage_kb(b + 1, cur ^ 1);
+      stage_kb(b + 1, (b + 1) & 1);
     }
-    const char* kt = lds + cur * BUF;
-    const char* vt = kt + KT_BYTES;
+    const char* kt = lds + (b & 1) * KT_BYTES;
 
     // S^T = K Q^T: st[kh] holds keys 32 kh + 8 (i / 4) + 4 hh + i % 4 (i = 0..15) of query q
     f32x16 st[2];
@@ -192,6 +218,7 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
         st[kh] = mfma32<DT>(kf, qf[s], st[kh]);
       }
     }
+    if (b > 0) pv(pf, (b - 1) % V_STAGES);
 
     // block max on the raw scores (the positive scale commutes with max); masked scores are -inf
     float bmax = -INFINITY;
@@ -200,7 +227,7 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
 #pragma unroll
       for (int i = 0; i < 16; i++) {
         float s = st[kh][i];
-        if constexpr (BIG) s += qb * kb_s[cur][kh * 32 + (i >> 2) * 8 + hh * 4 + (i & 3)];
+        if constexpr (BIG) s += qb * kb_s[(b & 1) * BKEYS + kh * 32 + (i >> 2) * 8 + hh * 4 + (i & 3)];
         if constexpr (MASK) {
           const int key = b * BKEYS + kh * 32 + (i >> 2) * 8 + hh * 4 + (i & 3);
           if (key >= p.Lk || (CAUSAL && key > q + p.q_pos0)) s = -INFINITY;
@@ -209,8 +236,9 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
         bmax = fmaxf(bmax, s);
       }
     bmax = fmaxf(bmax, __shfl_xor(bmax, 32)) * p.scale_log2;
-    // lazy max update (log2 units): only when some query of the wave grew by more than LAZY_TH; the
-    // condition is wave-uniform and read into a scalar so the rescale stays a branch, not 64 selects
+    // lazy max update (log2 units): only when some query of the wave grew by more than LAZY_TH (O then
+    // already holds block b - 1); the condition is wave-uniform and read into a scalar so the rescale
+    // stays a branch
     if (__builtin_amdgcn_readfirstlane(__any(bmax > m + LAZY_TH))) {
       const float m_new = fmaxf(m, bmax);
       asm volatile("" ::: "memory");  // not speculated: the compiler would otherwise multiply by 1 always
@@ -223,7 +251,6 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
 
     // P^T = exp2(s * scale_log2 - m) as the 16-bit B operand of O^T += V^T P^T (key step j uses
     // st[j / 2][8 (j & 1) ..]); the row sum accumulates the rounded P with v_dot2 (2 keys per op)
-    u32x4 pf[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
 #pragma unroll
@@ -234,19 +261,9 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
         l = dot2_ones<DT>(pf[j][e], l);
       }
     }
-#pragma unroll
-    for (int db = 0; db < 4; db++) {
-      const int d = db * 32 + l32;
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        // operand slots 0..3: key quad 4 j + hh, slots 4..7: quad 4 j + 2 + hh (one chunk, see vt_off)
-        const u32x4 vf = *(const u32x4*)(vt + vt_off(d, 4 * j + hh));
-        o[db] = mfma32<DT>(vf, pf[j], o[db]);
-      }
-    }
 
     if (has_next) {
-      store_vt(cur ^ 1);
+      store_vt((b + 1) % V_STAGES);  // the stage of block b - 2, whose P V ran in block b - 1
       __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));  // vmcnt(0): the next K tile has landed
     }
     lds_barrier();
@@ -258,6 +275,7 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
   int b = 0;
   for (; b < nfull; b++) process(b, std::false_type{});
   for (; b < nblk; b++) process(b, std::true_type{});
+  if (nblk > 0) pv(pf, (nblk - 1) % V_STAGES);
 
   // ---- normalise, gate, store: lane holds d = 32 db + 8 g + 4 hh + e of query q ----
   l += __shfl_xor(l, 32);
@@ -285,7 +303,7 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
 
 template <int DT, bool GATE, bool BIG>
 hipError_t launch3(bool causal, const AttnArgs& a, hipStream_t st) {
-  dim3 grid((a.Lq + BQ - 1) / BQ, a.heads), block(NTHR);
+  dim3 grid(((a.Lq + BQ - 1) / BQ) * a.heads), block(NTHR);
   if (causal)
     hipLaunchKernelGGL((attn_kernel<DT, GATE, BIG, true>), grid, block, 0, st, a);
   else
