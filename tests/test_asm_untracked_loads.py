@@ -1,0 +1,55 @@
+"""CPU check of the compiled GEMM kernels: no inline-asm load destination is touched before its wait, on
+any control-flow path of any instantiation (tests/asm_untracked_loads.py). Includes a self-test on a
+hand-written violation so the check cannot silently pass everything."""
+import os
+import shutil
+
+import pytest
+
+from tests.asm_untracked_loads import check_function, check_text, compile_to_asm
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CSRC = os.path.join(ROOT, "krea_image_amd", "csrc")
+
+BAD = """k:
+\t;;#ASMSTART
+\tglobal_load_dword v7, v[2:3], off
+\t;;#ASMEND
+\tv_add_u32_e32 v7, 1, v4
+\ts_waitcnt vmcnt(0)
+\ts_endpgm
+"""
+GOOD = """k:
+\t;;#ASMSTART
+\tglobal_load_dword v7, v[2:3], off
+\t;;#ASMEND
+\tglobal_load_dword v8, v[2:3], off
+\ts_waitcnt vmcnt(1)
+\tv_add_u32_e32 v7, 1, v7
+\ts_endpgm
+"""
+LOOP_BAD = """k:
+.LBB0_1:
+\tv_mov_b32_e32 v7, 0
+\t;;#ASMSTART
+\tglobal_load_dword v7, v[2:3], off
+\t;;#ASMEND
+\ts_cbranch_scc1 .LBB0_1
+\ts_waitcnt vmcnt(0)
+\ts_endpgm
+"""
+
+
+def test_checker_flags_known_violations():
+    assert check_function(BAD)
+    assert not check_function(GOOD)
+    assert check_function(LOOP_BAD)  # the write at the loop head hits the load of the previous iteration
+
+
+@pytest.mark.skipif(not os.path.exists("/opt/rocm/bin/hipcc"), reason="hipcc not available")
+def test_gemm_kernels_have_no_untracked_load_hazards(tmp_path):
+    text = compile_to_asm(os.path.join(CSRC, "kh_gemm.hip"), str(tmp_path / "gemm.s"), CSRC)
+    res = check_text(text)
+    assert len(res) >= 80, f"expected every GEMM instantiation, found {len(res)}"
+    bad = {k: v[:3] for k, v in res.items() if v}
+    assert not bad, f"inline-asm load destinations used before their wait: {bad}"
