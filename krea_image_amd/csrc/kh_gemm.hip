@@ -3,16 +3,18 @@
 //   acc[M, N] = X[M, K] (fp16 / bf16, row-major) x W~[K, N] (W stored input-major int8 or 16-bit), fp32.
 //
 // Semantics follow engine/kernels/gemm.metal:102-309 (gemm_tiled<EPI, QW, 0, 0>); the design is CDNA4's:
-//  * Block tile 256 (n) x 256 (m) x 64 (k), 512 threads = 8 wave64s in a 4 (n) x 2 (m) grid; each wave
-//    owns 64 n x 128 m = 2 x 4 MFMA blocks of v_mfma_f32_32x32x16_{f16,bf16}.
+//  * Block tile 256 (n) x 256 (m) x 64 (k), 512 threads = 8 wave64s (two per SIMD) in a 2 (n) x 4 (m) grid;
+//    each wave owns 128 n x 64 m = 4 x 2 MFMA blocks of v_mfma_f32_32x32x16_{f16,bf16}.
 //  * The MFMA "A" operand is the weight tile (rows n), "B" the activation tile (columns m), so each lane's
 //    accumulator holds 4 consecutive output columns n of one row m: epilogue loads of scale / bias / gate
 //    and the 16-bit or f32 stores are 8- or 16-byte vectors.
-//  * Both tiles live in LDS as [row][64 k] 16-bit with the 16-byte chunk index XOR-swizzled by (row & 7),
+//  * Both tiles live in LDS as [row][64 k] 16-bit with the 16-byte chunk index XOR-swizzled by swz(row),
 //    so the MFMA operand reads (one ds_read_b128 per lane: 8 consecutive k of one row) are conflict-free.
-//  * Weights: each thread loads 8 k-rows x 4 n-columns (a dword per int8 row, coalesced 256 B per wave
-//    and row), and converts them to 16-bit while transposing them in registers (v_perm_b32) into four
-//    16-byte k-vectors:
+//  * Activations stream global -> LDS by DMA (global_load_lds, no VGPR staging) through a 3-stage ring.
+//  * Weights: each thread loads 8 k-rows x 4 n-columns two K steps ahead (a dword per int8 row, coalesced
+//    256 B per wave and row; inline-asm loads with explicit waits), and converts them to 16-bit while
+//    transposing them in registers (v_perm_b32) into four 16-byte k-vectors, stored to a 2-stage LDS ring
+//    between the MFMA slices:
 //      - int8 per-channel, fp16 activations: 0x6400 | (q ^ 0x80) is the fp16 value 1024 + q + 128, so one
 //        packed subtract of 1152 gives q exactly (3 VALU ops per 2 weights); the per-channel scale is
 //        applied to the fp32 accumulator in the epilogue (q exact => no dequant rounding at all);
@@ -21,11 +23,11 @@
 //      - int8 with group scales (the reference's dit_q8 format): round16(fma(q + 128, s, -128 s)), which
 //        is the single-rounded f32 product q * s of gemm.metal:190-196 followed by one 16-bit rounding;
 //      - 16-bit weights: the same transpose, halfwords only.
-//  * Double-buffered LDS (2 x 64 KB): step t+1 is fetched into registers while step t is multiplied, then
-//    converted and stored into the other buffer; one workgroup barrier per K step.
+//    One workgroup barrier per K step; the loop body has no branches.
 //  * Tile order: block ids are first made contiguous per XCD (the dispatcher deals workgroups round-robin
 //    to the 8 XCDs, each with its own L2), then walked in groups of 8 tile rows, so co-resident
 //    workgroups of one XCD share both X row panels and W column panels in that XCD's L2.
+//  * Shapes whose tiles would fill under 60 % of a wave of workgroups run stream-K (see plan_launch).
 #include <cstdlib>
 #include <map>
 #include <mutex>
