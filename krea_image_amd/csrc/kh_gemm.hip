@@ -25,7 +25,7 @@
 //      - 16-bit weights: the same transpose, halfwords only.
 //    One workgroup barrier per K step; the loop body has no branches.
 //  * Tile order: block ids are first made contiguous per XCD (the dispatcher deals workgroups round-robin
-//    to the 8 XCDs, each with its own L2), then walked in groups of 8 tile rows, so co-resident
+//    to the 8 XCDs, each with its own L2), then walked in groups of 4 tile rows, so co-resident
 //    workgroups of one XCD share both X row panels and W column panels in that XCD's L2.
 //  * Shapes whose tiles would fill under 60 % of a wave of workgroups run stream-K (see plan_launch).
 #include <cstdlib>
@@ -48,7 +48,7 @@ constexpr int BM = 256, BN = 256, BK = 64;
 constexpr int WAVES_DEFAULT = KH_GEMM_WAVES;
 constexpr int STAGE = BM * BK * 2;  // bytes of one 16-bit 256 x 64 tile
 constexpr int X_STAGES = 3, W_STAGES = 2;
-constexpr int GROUP_M = 8;
+constexpr int GROUP_M = 4;  // tile rows per group (measured: 4 edges out 2, 8 and 16 by 1-3 %)
 
 // weight formats; the group formats carry their scale type in the kernel so the K loop has no branches
 enum { WF_16 = 0, WF_I8_CHANNEL = 1, WF_I8_GROUP = 2, WF_I8_GROUP_F16 = 3, WF_I8_GROUP_BF16 = 4 };
