@@ -61,6 +61,29 @@ __device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, const f
                                                   0);
 }
 
+// Combine the value of lane l with that of lane l ^ 32 (the two lanes holding the two key halves of one query)
+// with v_permlane32_swap: a VALU lane exchange instead of an LDS-routed shuffle on the softmax's critical
+// path. Swapping the upper half of one copy of x with the lower half of another leaves x_lo[l % 32] in the
+// first and x_hi[l % 32] in the second at every lane, so both lanes compute the same expression. (Written
+// as asm: the compiler builtin with one value for both operands folded the two results into one.)
+__device__ __forceinline__ void swap_halves(float x, float& lo, float& hi) {
+  lo = x;
+  hi = x;
+  // the wait states around it are the ones the compiler inserts for the builtin form (VALU write -> swap
+  // read, swap write -> VALU read); inside asm it cannot see the hazard
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(lo), "+v"(hi));
+}
+__device__ __forceinline__ float max_halves(float x) {
+  float lo, hi;
+  swap_halves(x, lo, hi);
+  return fmaxf(lo, hi);
+}
+__device__ __forceinline__ float sum_halves(float x) {
+  float lo, hi;
+  swap_halves(x, lo, hi);
+  return lo + hi;
+}
+
 // acc + lo + hi of a packed 16-bit pair (v_dot2c_f32_{f16,bf16} against (1, 1))
 template <int DT>
 __device__ __forceinline__ float dot2_ones(uint32_t pr, float acc) {
@@ -235,7 +258,7 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
         st[kh][i] = s;
         bmax = fmaxf(bmax, s);
       }
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32)) * p.scale_log2;
+    bmax = max_halves(bmax) * p.scale_log2;
     // lazy max update (log2 units): only when some query of the wave grew by more than LAZY_TH (O then
     // already holds block b - 1); the condition is wave-uniform and read into a scalar so the rescale
     // stays a branch
@@ -278,7 +301,7 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
   if (nblk > 0) pv(pf, (nblk - 1) % V_STAGES);
 
   // ---- normalise, gate, store: lane holds d = 32 db + 8 g + 4 hh + e of query q ----
-  l += __shfl_xor(l, 32);
+  l = sum_halves(l);
   if (q >= p.Lq) return;
   const float inv = l > 0.f ? 1.0f / l : 0.f;
   uint16_t* op = (uint16_t*)p.O + (size_t)q * p.ldo + h * D;
