@@ -254,12 +254,16 @@ class QwDit(DitRunner):
 
 
 def bench_step(dev, rows_img: int = 4096, rows_txt: int = 512, layers: int = 71, steps: int = 3,
-               shape: Optional[DitShape] = None) -> dict:
-    """Latency of one full denoising step (embed + all layers + head) at the given token count."""
+               shape: Optional[DitShape] = None, grid: Optional[tuple] = None) -> dict:
+    """Latency of one full denoising step (embed + all layers + head) at the given token count; the image
+    tokens form an H x W latent grid (square by default)."""
     shape = shape or baseline_shape(layers)
-    side = int(round(rows_img ** 0.5))
-    assert side * side == rows_img
-    run = DitRunner(shape, rows_txt, side, side, dev)
+    if grid is None:
+        side = int(round(rows_img ** 0.5))
+        grid = (side, side)
+    if grid[0] * grid[1] != rows_img:
+        raise ValueError(f"grid {grid} does not hold {rows_img} image tokens")
+    run = DitRunner(shape, rows_txt, grid[0], grid[1], dev)
     gen = torch.Generator(device=dev)
     gen.manual_seed(1)
     txt = torch.randn(rows_txt, shape.dim, generator=gen, device=dev)
