@@ -40,8 +40,8 @@ PEAK_TFLOPS = 2500.0  # MI355X dense fp16 / bf16 MFMA
 FLOP_UP = 2.0 * M * D * FF
 FLOP_DOWN = 2.0 * M * FF * D
 # HBM bytes per up-projection launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, each scaled by the same
-# counter's reading for a 512 MiB copy (profiles/gemm_up_traffic_4096x3072x12288.md): 377.8 MB + 100.7 MB.
-UP_TRAFFIC_BYTES = 478.5e6
+# counter's reading for a 512 MiB copy (profiles/gemm_up_traffic_4096x3072x12288.md): 302.3 MB + 100.7 MB.
+UP_TRAFFIC_BYTES = 403.0e6
 
 
 def make_inputs(dev, seed=1234):
@@ -144,9 +144,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-dit", action="store_true", help="skip the full DiT step latency")
-    ap.add_argument("--probe", action="store_true",
-                    help="profiling probe: one up-projection launch and one 512 MiB device copy (for rocprofv3 "
-                         "--pmc FETCH_SIZE / WRITE_SIZE calibration), no JSON line")
+    ap.add_argument("--probe", nargs="?", const="gemm", choices=["gemm", "attention", "dit"],
+                    help="profiling probe, no JSON line: 'gemm' = one up-projection launch and one 512 MiB device "
+                         "copy (for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE calibration); 'attention' = three "
+                         "launches of the joint attention of config [2] (4608 tokens x 24 heads, fp16); 'dit' = two full "
+                         "DiT steps at 1024^2 (71 blocks)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the dequant-GEMM path has no multi-GPU mode in this build "
@@ -170,6 +172,22 @@ def main():
         if ev is not None:
             ev[2].record(stream)
 
+    if args.probe == "dit":
+        from krea_image_amd import dit
+        dit.bench_step(dev, rows_img=4096, rows_txt=512, layers=71, steps=2)
+        return
+    if args.probe == "attention":
+        g = torch.Generator(device=dev)
+        g.manual_seed(7)
+        L, Hh = 4608, 24
+        qkv = torch.randn(L, 3 * Hh * 128, generator=g, device=dev).half()
+        O = torch.empty(L, Hh * 128, device=dev, dtype=torch.float16)
+        ld = 3 * Hh * 128
+        for _ in range(3):
+            kh.attention(qkv[:, :Hh * 128], qkv[:, Hh * 128:2 * Hh * 128], qkv[:, 2 * Hh * 128:], O, L, L, Hh, ld, ld,
+                         ld, Hh * 128)
+        torch.cuda.synchronize()
+        return
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
