@@ -20,9 +20,9 @@ Reported beside it:
   configs      : the other BASELINE configs on the GPU, each timed with HIP events on the launch stream:
                  [0] one dequant-GEMM 4096 x 3072 x 3072 + fp16 bias, [2] joint attention 4608 tokens x 24
                  heads, [3] one DiT block at 4608 rows, [4] the full step swept over 1024 / 4096 / 8192
-                 image tokens + 512 text tokens.
+                 image tokens + 512 text tokens; and the VAE decode of a 64 x 64 latent to 1024^2 RGBA.
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-dit] [--probe]
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-dit] [--probe {gemm,attention,dit,vae}]
 """
 import argparse
 import json
@@ -115,7 +115,27 @@ def other_configs(dev):
         sweep[str(img)] = {"ms": info["ms"], "rows": info["rows"], "tflops": info["tflops"]}
     out["dit_step_sweep"] = sweep
     torch.cuda.empty_cache()
+    out["vae_decode_1024sq"] = vae_decode_bench(dev)
     return out
+
+
+def vae_decode_bench(dev, iters=5):
+    """VAE decode of a 64 x 64 latent (1024 x 1024 RGBA8) from a random-init vae.qw (the converter's tensor
+    names and shapes)."""
+    import tempfile
+    from krea_image_amd import qw, vae
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "vae.qw")
+        vae.write_random_vae(path, seed=5)
+        with qw.QwFile(path) as f:
+            f.upload()
+            dec = vae.VaeDecoder(f, dev)
+            z = torch.randn(64 * 64, 64, device=dev)
+            ms = _event_ms(lambda: dec.decode(z, 64, 64), iters, warm=2)
+            del dec
+    flops = vae.decode_flops(64, 64)
+    return {"ms": round(ms, 3), "tflops": round(flops / ms / 1e9, 1), "gflop": round(flops / 1e9, 1),
+            "workspace_mb": round(vae.workspace_bytes(64, 64) / 2 ** 20, 1)}
 
 
 def cpu_baseline(X, x, Wup, Wdown):
@@ -144,11 +164,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-dit", action="store_true", help="skip the full DiT step latency")
-    ap.add_argument("--probe", nargs="?", const="gemm", choices=["gemm", "attention", "dit"],
+    ap.add_argument("--probe", nargs="?", const="gemm", choices=["gemm", "attention", "dit", "vae"],
                     help="profiling probe, no JSON line: 'gemm' = one up-projection launch and one 512 MiB device "
                          "copy (for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE calibration); 'attention' = three "
                          "launches of the joint attention of config [2] (4608 tokens x 24 heads, fp16); 'dit' = two full "
-                         "DiT steps at 1024^2 (71 blocks)")
+                         "DiT steps at 1024^2 (71 blocks); 'vae' = the VAE decode of a 64 x 64 "
+                         "latent (1024^2 RGBA), 2 + 5 calls")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the dequant-GEMM path has no multi-GPU mode in this build "
@@ -175,6 +196,9 @@ def main():
     if args.probe == "dit":
         from krea_image_amd import dit
         dit.bench_step(dev, rows_img=4096, rows_txt=512, layers=71, steps=2)
+        return
+    if args.probe == "vae":
+        print(json.dumps(vae_decode_bench(dev)), flush=True)
         return
     if args.probe == "attention":
         g = torch.Generator(device=dev)

@@ -212,6 +212,36 @@ int kh_free(void* p);
 int kh_upload(kh_stream s, void* dst, const void* src, size_t bytes, char* err, int errlen);   /* H2D, synchronous */
 int kh_download(kh_stream s, void* dst, const void* src, size_t bytes, char* err, int errlen); /* D2H, synchronous */
 
+/* ---- VAE decoder (Qwen-Image / Wan 2.1 VAE, single frame), NHWC bf16 activations [pixel, channel] ----
+ * The convolutions run on kh_gemm (im2col panels in HBM x the converter's Wt[(ky*3+kx)*Cin + ci, co]
+ * bf16 weights, tools/convert.py:338-344); these are the steps around them. */
+/* 3x3 (zero padding 1) im2col of output pixels [m0, m0 + rows) of an H x W output: col[r, tap * C + ci],
+ * columns [9 C, Kpad) zero; up = 1: x is H/2 x W/2 and nearest-upsampled (the vconv A loader,
+ * engine/kernels/vae.metal:11-28). C, ldx, Kpad multiples of 8. */
+int kh_vae_im2col(kh_stream stream, const void* x, int ldx, int C, int H, int W, int up, int m0, int rows, void* col,
+                  int Kpad, char* err, int errlen);
+/* y = x sqrt(C) / max(||x||, 1e-12) * gamma (+ SiLU) per pixel (vae_norm_silu, vae.metal:588-668). */
+int kh_vae_norm_silu(kh_stream stream, const void* x, int ldx, const float* gamma, void* y, int ldy, int P, int C,
+                     int silu, char* err, int errlen);
+/* DiT latent tokens f32 [H16 W16, 64] -> VAE input bf16 [2 H16 x 2 W16, 16]: de-normalize (z std + mean) and
+ * post_quant_conv (w f32 [in][out] 16 x 16, b [16]) (vae_unpack_pq, vae.metal:690-712). */
+int kh_vae_unpack(kh_stream stream, const float* z, const float* mean, const float* stdv, const float* w,
+                  const float* b, void* y, int H16, int W16, char* err, int errlen);
+/* P[r, :n] = bf16(softmax(S[r, :n] * scale)) for rows r < rows, row stride ld (softmax_rows, vae.metal:727-757). */
+int kh_vae_softmax(kh_stream stream, const float* S, int ld, int rows, int n, float scale, void* P, char* err,
+                   int errlen);
+/* RGBA8 = quantize(clamp(conv3x3(x, w [9 C, 4] bf16) + bias[4], -1, 1)) (vae_conv_out_rgba, vae.metal:759-785). */
+int kh_vae_conv_out(kh_stream stream, const void* x, int ldx, int C, const void* w, const float* bias, void* rgba,
+                    int H, int W, char* err, int errlen);
+/* Device workspace kh_vae_decode needs for a H16 x W16 latent (0 for an empty one). */
+size_t kh_vae_workspace_bytes(int H16, int W16);
+/* Full decode (VAEDecoder::run, engine/src/vae.mm:289-337): z f32 [H16 W16, 64] -> rgba uint8 [16 H16 x 16 W16, 4]
+ * on the device. Weights come from an uploaded vae.qw (kh_qw_upload), by the converter's tensor names. The
+ * workspace (256-byte aligned, >= kh_vae_workspace_bytes) holds every intermediate; the only allocation is the
+ * GEMM stream-K workspace of kh_gemm, made once per stream. */
+int kh_vae_decode(kh_stream stream, const kh_qw* vae, const float* z, int H16, int W16, void* workspace,
+                  size_t workspace_bytes, void* rgba, char* err, int errlen);
+
 /* Library identification (for the loader checks of the host bindings). */
 const char* kh_version(void);
 

@@ -80,4 +80,49 @@ int kh_dit_forward(kh_stream stream, const kh_dit_config* cfg, const kh_dit_laye
   return kh::dit_forward((hipStream_t)stream, *cfg, layers, n_layers, *state, rows, e);
 }
 
+/* ---- VAE decoder ---- */
+int kh_vae_im2col(kh_stream stream, const void* x, int ldx, int C, int H, int W, int up, int m0, int rows, void* col,
+                  int Kpad, char* err, int errlen) {
+  kh::Err e{err, errlen};
+  e.clear();
+  return kh::vae_im2col((hipStream_t)stream, x, ldx, C, H, W, up, m0, rows, col, Kpad, e);
+}
+
+int kh_vae_norm_silu(kh_stream stream, const void* x, int ldx, const float* gamma, void* y, int ldy, int P, int C,
+                     int silu, char* err, int errlen) {
+  kh::Err e{err, errlen};
+  e.clear();
+  return kh::vae_norm_silu((hipStream_t)stream, x, ldx, gamma, y, ldy, P, C, silu, e);
+}
+
+int kh_vae_unpack(kh_stream stream, const float* z, const float* mean, const float* stdv, const float* w,
+                  const float* b, void* y, int H16, int W16, char* err, int errlen) {
+  kh::Err e{err, errlen};
+  e.clear();
+  return kh::vae_unpack((hipStream_t)stream, z, mean, stdv, w, b, y, H16, W16, e);
+}
+
+int kh_vae_softmax(kh_stream stream, const float* S, int ld, int rows, int n, float scale, void* P, char* err,
+                   int errlen) {
+  kh::Err e{err, errlen};
+  e.clear();
+  return kh::vae_softmax((hipStream_t)stream, S, ld, rows, n, scale, P, e);
+}
+
+int kh_vae_conv_out(kh_stream stream, const void* x, int ldx, int C, const void* w, const float* bias, void* rgba,
+                    int H, int W, char* err, int errlen) {
+  kh::Err e{err, errlen};
+  e.clear();
+  return kh::vae_conv_out((hipStream_t)stream, x, ldx, C, w, bias, rgba, H, W, e);
+}
+
+size_t kh_vae_workspace_bytes(int H16, int W16) { return kh::vae_workspace_bytes(H16, W16); }
+
+int kh_vae_decode(kh_stream stream, const kh_qw* vae, const float* z, int H16, int W16, void* workspace,
+                  size_t workspace_bytes, void* rgba, char* err, int errlen) {
+  kh::Err e{err, errlen};
+  e.clear();
+  return kh::vae_decode((hipStream_t)stream, vae, z, H16, W16, workspace, workspace_bytes, rgba, e);
+}
+
 }  // extern "C"

@@ -56,4 +56,22 @@ int dit_forward(hipStream_t st, const kh_dit_config& c, const kh_dit_layer* laye
                 int R, Err& e);
 int rope_tables(int T, int H, int W, int mode, float* cosb, float* sinb);
 
+int vae_unpack(hipStream_t st, const float* z, const float* mean, const float* stdv, const float* w, const float* b,
+               void* y, int H16, int W16, Err& e);
+int vae_im2col(hipStream_t st, const void* x, int ldx, int C, int H, int W, int up, int m0, int rows, void* col,
+               int Kpad, Err& e);
+int vae_norm_silu(hipStream_t st, const void* x, int ldx, const float* gamma, void* y, int ldy, int P, int C, int silu,
+                  Err& e);
+int vae_add(hipStream_t st, void* y, const void* a, long long n, Err& e);
+int vae_transpose(hipStream_t st, const void* in, int ld, int off, int P, int C, void* out, int ldo, Err& e);
+int vae_softmax(hipStream_t st, const float* S, int ld, int rows, int n, float scale, void* Pm, Err& e);
+int vae_conv_out(hipStream_t st, const void* x, int ldx, int C, const void* w, const float* bias, void* rgba, int H,
+                 int W, Err& e);
+int vae_zero(hipStream_t st, void* p, size_t bytes, Err& e);
+int vae_pad_weight(hipStream_t st, const void* w, int K, int N, void* out, int Kp, int Np, const float* b, float* bout,
+                   Err& e);
+size_t vae_workspace_bytes(int H16, int W16);
+int vae_decode(hipStream_t st, const kh_qw* f, const float* z, int H16, int W16, void* ws, size_t ws_bytes, void* rgba,
+               Err& e);
+
 }  // namespace kh

@@ -504,3 +504,118 @@ void or_attention(const void* Q, const void* K, const void* V, void* O, int dtyp
   free(Kf);
   free(Vf);
 }
+
+/* ---------------------------------------------------------------------------------------------- */
+/* VAE decoder ops (engine/kernels/vae.metal), NHWC bf16 activations [pixel, channel].            */
+
+/* vconv (vae.metal:5-128): out[p, n] = bf16(bias[n] + sum_{tap, ci} in[src(p, tap), ci] * Wt[tap*Cin + ci, n]
+ * (+ res[p, n])), fp32 accumulation; ks = 1 or 3 (zero padding ks / 2); up = 1: the input is H/2 x W/2,
+ * nearest-upsampled. The residual joins the fp32 sum before the single 16-bit rounding. */
+void or_vae_conv(const uint16_t* x, int H, int W, int Cin, int ks, int up, const uint16_t* w, const float* bias,
+                 const uint16_t* res, int N, uint16_t* y) {
+  const int Win = up ? W / 2 : W;
+  float* wf = (float*)malloc((size_t)ks * ks * Cin * N * sizeof(float));
+  for (size_t i = 0; i < (size_t)ks * ks * Cin * N; i++) wf[i] = or_bf16_to_f32(w[i]);
+#pragma omp parallel for schedule(static)
+  for (int p = 0; p < H * W; p++) {
+    const int py = p / W, px = p % W;
+    float acc[1024];
+    for (int n0 = 0; n0 < N; n0 += 1024) {  /* output channels in blocks of 1024 */
+      const int nb = N - n0 < 1024 ? N - n0 : 1024;
+      for (int n = 0; n < nb; n++) acc[n] = 0.f;
+      for (int tap = 0; tap < ks * ks; tap++) {
+        int sy = py + (ks == 3 ? tap / 3 - 1 : 0), sx = px + (ks == 3 ? tap % 3 - 1 : 0);
+        if (sy < 0 || sy >= H || sx < 0 || sx >= W) continue;
+        if (up) {
+          sy >>= 1;
+          sx >>= 1;
+        }
+        const uint16_t* xi = x + ((size_t)sy * Win + sx) * Cin;
+        const float* wt = wf + (size_t)tap * Cin * N + n0;
+        for (int ci = 0; ci < Cin; ci++) {
+          const float a = or_bf16_to_f32(xi[ci]);
+          const float* wr = wt + (size_t)ci * N;
+          for (int n = 0; n < nb; n++) acc[n] += a * wr[n];
+        }
+      }
+      for (int n = 0; n < nb; n++) {
+        float v = acc[n] + bias[n0 + n];
+        if (res) v += or_bf16_to_f32(res[(size_t)p * N + n0 + n]);
+        y[(size_t)p * N + n0 + n] = or_f32_to_bf16(v);
+      }
+    }
+  }
+  free(wf);
+}
+
+/* vae_norm_silu (vae.metal:588-621): y = x * sqrt(C) / max(||x||, 1e-12) * gamma, SiLU optional. */
+void or_vae_norm_silu(const uint16_t* x, const float* gamma, uint16_t* y, int P, int C, int silu) {
+#pragma omp parallel for schedule(static)
+  for (int p = 0; p < P; p++) {
+    const uint16_t* xr = x + (size_t)p * C;
+    float ss = 0.f;
+    for (int c = 0; c < C; c++) {
+      const float v = or_bf16_to_f32(xr[c]);
+      ss += v * v;
+    }
+    const float scale = sqrtf((float)C) / fmaxf(sqrtf(ss), 1e-12f);
+    for (int c = 0; c < C; c++) {
+      float t = or_bf16_to_f32(xr[c]) * scale * gamma[c];
+      if (silu) t = silu_f(t);
+      y[(size_t)p * C + c] = or_f32_to_bf16(t);
+    }
+  }
+}
+
+/* vae_unpack_pq (vae.metal:690-712) */
+void or_vae_unpack(const float* z, const float* mean, const float* stdv, const float* w, const float* b, uint16_t* y,
+                   int H16, int W16) {
+  const int W2 = 2 * W16;
+  for (int pix = 0; pix < 4 * H16 * W16; pix++) {
+    const int yy = pix / W2, xx = pix % W2;
+    const float* zt = z + (size_t)((yy >> 1) * W16 + (xx >> 1)) * 64 + (yy & 1) * 2 + (xx & 1);
+    float u[16];
+    for (int c = 0; c < 16; c++) u[c] = zt[c * 4] * stdv[c] + mean[c];
+    for (int o = 0; o < 16; o++) {
+      float acc = b[o];
+      for (int c = 0; c < 16; c++) acc += w[c * 16 + o] * u[c];
+      y[(size_t)pix * 16 + o] = or_f32_to_bf16(acc);
+    }
+  }
+}
+
+/* softmax_rows (vae.metal:727-757): P[r, :n] = bf16(softmax(S[r, :n] * scale)) */
+void or_vae_softmax(const float* S, int ld, int rows, int n, float scale, uint16_t* P) {
+#pragma omp parallel for schedule(static)
+  for (int r = 0; r < rows; r++) {
+    const float* s = S + (size_t)r * ld;
+    float mx = -INFINITY;
+    for (int i = 0; i < n; i++) mx = fmaxf(mx, s[i] * scale);
+    double sum = 0.0;
+    for (int i = 0; i < n; i++) sum += expf(s[i] * scale - mx);
+    const float inv = (float)(1.0 / sum);
+    for (int i = 0; i < n; i++) P[(size_t)r * ld + i] = or_f32_to_bf16(expf(s[i] * scale - mx) * inv);
+  }
+}
+
+/* vae_conv_out_rgba (vae.metal:759-785) */
+void or_vae_conv_out(const uint16_t* x, int C, const uint16_t* w, const float* bias, uint8_t* rgba, int H, int W) {
+#pragma omp parallel for schedule(static)
+  for (int pix = 0; pix < H * W; pix++) {
+    const int y = pix / W, xx = pix % W;
+    float acc[4] = {bias[0], bias[1], bias[2], bias[3]};
+    for (int tap = 0; tap < 9; tap++) {
+      const int sy = y + tap / 3 - 1, sx = xx + tap % 3 - 1;
+      if (sy < 0 || sy >= H || sx < 0 || sx >= W) continue;
+      const uint16_t* ip = x + ((size_t)sy * W + sx) * C;
+      const uint16_t* wp = w + (size_t)tap * C * 4;
+      for (int c = 0; c < C; c++)
+        for (int k = 0; k < 4; k++) acc[k] += or_bf16_to_f32(ip[c]) * or_bf16_to_f32(wp[(size_t)c * 4 + k]);
+    }
+    for (int k = 0; k < 4; k++) {
+      float a = fminf(fmaxf(acc[k], -1.f), 1.f);
+      a = rintf(fminf(fmaxf(a * 0.5f + 0.5f, 0.f), 1.f) * 255.f);
+      rgba[(size_t)pix * 4 + k] = (uint8_t)a;
+    }
+  }
+}

@@ -80,6 +80,15 @@ void or_attention(const void* Q, const void* K, const void* V, void* O, int dtyp
                   int ldk, int ldv, int ldo, int group, int causal, int q_pos0, const void* G, int ldg, const float* QB,
                   const float* KB, int threads);
 
+/* ---- VAE decoder ops (engine/kernels/vae.metal) ---- */
+void or_vae_conv(const uint16_t* x, int H, int W, int Cin, int ks, int up, const uint16_t* w, const float* bias,
+                 const uint16_t* res, int N, uint16_t* y);
+void or_vae_norm_silu(const uint16_t* x, const float* gamma, uint16_t* y, int P, int C, int silu);
+void or_vae_unpack(const float* z, const float* mean, const float* stdv, const float* w, const float* b, uint16_t* y,
+                   int H16, int W16);
+void or_vae_softmax(const float* S, int ld, int rows, int n, float scale, uint16_t* P);
+void or_vae_conv_out(const uint16_t* x, int C, const uint16_t* w, const float* bias, uint8_t* rgba, int H, int W);
+
 #ifdef __cplusplus
 }
 #endif

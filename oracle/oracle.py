@@ -43,6 +43,12 @@ def lib():
         _lib.or_qk_norm_rope.argtypes = ([ctypes.c_void_p, ctypes.c_int] + [ctypes.c_void_p] * 4 +
                                          [ctypes.c_int] * 6 + [ctypes.c_float, ctypes.c_int, ctypes.c_int] +
                                          [ctypes.c_void_p] * 2)
+        vp, i = ctypes.c_void_p, ctypes.c_int
+        _lib.or_vae_conv.argtypes = [vp, i, i, i, i, i, vp, vp, vp, i, vp]
+        _lib.or_vae_norm_silu.argtypes = [vp, vp, vp, i, i, i]
+        _lib.or_vae_unpack.argtypes = [vp] * 6 + [i, i]
+        _lib.or_vae_softmax.argtypes = [vp, i, i, i, ctypes.c_float, vp]
+        _lib.or_vae_conv_out.argtypes = [vp, i, vp, vp, vp, i, i]
     return _lib
 
 
@@ -218,3 +224,44 @@ def attention(Q, K, V, dtype, heads, group=1, causal=0, q_pos0=0, G=None, QB=Non
                        _p(None if QB is None else np.ascontiguousarray(QB, np.float32)),
                        _p(None if KB is None else np.ascontiguousarray(KB, np.float32)), threads)
     return O
+
+
+# ---- VAE decoder ops (engine/kernels/vae.metal); bf16 tensors as uint16 bit patterns ----
+def vae_conv(x, H, W, w, bias, N, ks=3, up=0, res=None):
+    """x [Hin*Win, Cin] bf16 -> [H*W, N] bf16; w [ks*ks*Cin, N] bf16, bias [N] f32 (vae.metal:5-128)."""
+    x = np.ascontiguousarray(x, np.uint16)
+    Cin = x.shape[1]
+    y = np.empty((H * W, N), np.uint16)
+    lib().or_vae_conv(_p(x), H, W, Cin, ks, up, _p(np.ascontiguousarray(w, np.uint16)),
+                      _p(np.ascontiguousarray(bias, np.float32)),
+                      _p(None if res is None else np.ascontiguousarray(res, np.uint16)), N, _p(y))
+    return y
+
+
+def vae_norm_silu(x, gamma, silu=1):
+    x = np.ascontiguousarray(x, np.uint16)
+    y = np.empty_like(x)
+    lib().or_vae_norm_silu(_p(x), _p(np.ascontiguousarray(gamma, np.float32)), _p(y), x.shape[0], x.shape[1], silu)
+    return y
+
+
+def vae_unpack(z, mean, stdv, w, b, H16, W16):
+    y = np.empty((4 * H16 * W16, 16), np.uint16)
+    f = lambda a: np.ascontiguousarray(a, np.float32)  # noqa: E731
+    lib().or_vae_unpack(_p(f(z)), _p(f(mean)), _p(f(stdv)), _p(f(w)), _p(f(b)), _p(y), H16, W16)
+    return y
+
+
+def vae_softmax(S, n, scale):
+    S = np.ascontiguousarray(S, np.float32)
+    P = np.zeros(S.shape, np.uint16)
+    lib().or_vae_softmax(_p(S), S.shape[1], S.shape[0], n, scale, _p(P))
+    return P
+
+
+def vae_conv_out(x, w, bias, H, W):
+    x = np.ascontiguousarray(x, np.uint16)
+    rgba = np.empty((H * W, 4), np.uint8)
+    lib().or_vae_conv_out(_p(x), x.shape[1], _p(np.ascontiguousarray(w, np.uint16)),
+                          _p(np.ascontiguousarray(bias, np.float32)), _p(rgba), H, W)
+    return rgba
