@@ -17,6 +17,8 @@ Reported beside it:
                  params of hidden 3072), the metric's second half (target < 500 ms).
   dit_step_reference : the same step on the reference architecture (hidden 6144, GQA 48/12, gated
                  attention, SwiGLU, 28 blocks, group-128 int8), a secondary line.
+  library_reference : torch.matmul (hipBLASLt) on the same two shapes with fp16 weights and no epilogue,
+                 timed the same way: what the vendor library sustains here, as context for the roofline.
   configs      : the other BASELINE configs on the GPU, each timed with HIP events on the launch stream:
                  [0] one dequant-GEMM 4096 x 3072 x 3072 + fp16 bias, [2] joint attention 4608 tokens x 24
                  heads, [3] one DiT block at 4608 rows, [4] the full step swept over 1024 / 4096 / 8192
@@ -136,6 +138,21 @@ def vae_decode_bench(dev, iters=5):
     flops = vae.decode_flops(64, 64)
     return {"ms": round(ms, 3), "tflops": round(flops / ms / 1e9, 1), "gflop": round(flops / 1e9, 1),
             "workspace_mb": round(vae.workspace_bytes(64, 64) / 2 ** 20, 1)}
+
+
+def library_reference(dev, X, Wup, Wdown, H):
+    """The same two shapes as plain fp16 GEMMs in torch.matmul (hipBLASLt on ROCm), weights already in fp16
+    (the int8 values widened: no dequant, no epilogue). Context for the roofline fraction: what the vendor
+    library sustains on this box for the same contraction, not a measurement of this build."""
+    Wu16, Wd16 = Wup.w.to(torch.float16), Wdown.w.to(torch.float16)
+    Yu = torch.empty(M, FF, device=dev, dtype=torch.float16)
+    Yd = torch.empty(M, D, device=dev, dtype=torch.float16)
+    up = _event_ms(lambda: torch.matmul(X, Wu16, out=Yu), 20, warm=5)
+    down = _event_ms(lambda: torch.matmul(H, Wd16, out=Yd), 20, warm=5)
+    del Wu16, Wd16, Yu, Yd
+    return {"kind": "torch.matmul fp16 (hipBLASLt), same shapes, weights pre-widened to fp16, no epilogue",
+            "up_ms": round(up, 4), "up_tflops": round(FLOP_UP / up / 1e9, 1),
+            "down_ms": round(down, 4), "down_tflops": round(FLOP_DOWN / down / 1e9, 1)}
 
 
 def cpu_baseline(X, x, Wup, Wdown):
@@ -266,6 +283,7 @@ def main():
                      "frac": round(up_tflops / PEAK_TFLOPS, 4), "traffic": UP_TRAFFIC_BYTES,
                      "kernel": "kh gemm_kernel<f16, int8 per-channel, GELU> (up-projection, 309.24 GFLOP/launch)"},
     }
+    out["library_reference"] = library_reference(dev, X, Wup, Wdown, H)
     if not args.no_dit:
         from krea_image_amd import dit
         step_info = dit.bench_step(dev, rows_img=4096, rows_txt=512, layers=71)

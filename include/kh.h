@@ -66,7 +66,10 @@ typedef struct kh_weight {
  * steps spread over one workgroup per CU); those launches use a workspace of 2 x CUs x 256 KiB + 256 KiB
  * that kh_gemm allocates once per (device, stream) on first need and keeps until the process ends (on a
  * capturing stream without one, the launch stays data-parallel). Results are deterministic either way.
- * KH_GEMM_STREAMK=0 in the environment keeps every launch data-parallel.
+ * KH_GEMM_STREAMK=0 in the environment keeps every launch data-parallel. A data-parallel launch whose 256 x 256
+ * tiles fill only part of one wave of workgroups uses 256 x 192 tiles when N % 192 == 0 and they still fit in
+ * one wave (not for SWIGLU); KH_GEMM_TN192=0 keeps 256-wide tiles. Either tile sums each output's products in
+ * the same order, so the results are bitwise identical.
  * Replaces krea::Metal::gemm (engine/src/metal.h:66-69, engine/src/metal.mm:146-163). */
 int kh_gemm(kh_stream stream, int epi, const void* A, int a_dtype, const kh_weight* W, void* C, int M, int N, int K,
             int lda, int ldw, int ldc, const void* vec, char* err, int errlen);

@@ -54,15 +54,17 @@ __device__ __forceinline__ float gelu_tanh_f(float x) {
   const float k0 = 0.7978845608028654f, k1 = 0.044715f;
   return 0.5f * x * (1.0f + tanhf(k0 * (x + k1 * x * x * x)));
 }
-// Epilogue forms on the hardware exp / reciprocal (v_exp_f32, v_rcp_f32, ~1 ulp each):
+// Epilogue forms on the hardware exp2 / reciprocal (v_exp_f32, v_rcp_f32, ~1 ulp each):
 //   gelu_tanh(x) = 0.5 x (1 + tanh(u)) = x / (1 + e^(-2u)),  u = k0 (x + k1 x^3)
+//                = x / (1 + 2^(x (c0 + c1 x^2))),  c0 = -2 k0 log2(e), c1 = -2 k0 k1 log2(e)
 //   silu(x) = x / (1 + e^(-x))
-// Both saturate correctly: e^(...) -> inf gives -0, e^(...) -> 0 gives x.
+// Both saturate correctly: 2^(...) -> inf gives -0, 2^(...) -> 0 gives x.
 __device__ __forceinline__ float rcp_fast(float x) { return __builtin_amdgcn_rcpf(x); }
 __device__ __forceinline__ float gelu_fast(float x) {
-  const float k0 = 0.7978845608028654f, k1 = 0.044715f;
-  const float u = k0 * (x + k1 * x * x * x);
-  return x * rcp_fast(1.0f + __expf(-2.0f * u));
+  constexpr double k0 = 0.7978845608028654, k1 = 0.044715, log2e = 1.4426950408889634;
+  constexpr float c0 = (float)(-2.0 * k0 * log2e), c1 = (float)(-2.0 * k0 * k1 * log2e);
+  const float t = __builtin_fmaf(x * x, c1, c0);
+  return x * rcp_fast(1.0f + __builtin_amdgcn_exp2f(t * x));
 }
 __device__ __forceinline__ float silu_fast(float x) { return x * rcp_fast(1.0f + __expf(-x)); }
 __device__ __forceinline__ float sigmoid_fast(float x) { return rcp_fast(1.0f + __expf(-x)); }

@@ -4,7 +4,8 @@
 //
 // Semantics follow engine/kernels/gemm.metal:102-309 (gemm_tiled<EPI, QW, 0, 0>); the design is CDNA4's:
 //  * Block tile 256 (n) x 256 (m) x 64 (k), 512 threads = 8 wave64s (two per SIMD) in a 2 (n) x 4 (m) grid;
-//    each wave owns 128 n x 64 m = 4 x 2 MFMA blocks of v_mfma_f32_32x32x16_{f16,bf16}.
+//    each wave owns 128 n x 64 m = 4 x 2 MFMA blocks of v_mfma_f32_32x32x16_{f16,bf16}. A 192 (n) x 256 (m)
+//    variant (waves 96 n x 64 m) serves shapes whose 256-wide tiles would leave CUs idle (see plan_launch).
 //  * The MFMA "A" operand is the weight tile (rows n), "B" the activation tile (columns m), so each lane's
 //    accumulator holds 4 consecutive output columns n of one row m: epilogue loads of scale / bias / gate
 //    and the 16-bit or f32 stores are 8- or 16-byte vectors.
@@ -165,9 +166,14 @@ struct Cfg {
   static constexpr int LOADS = X_LOADS + KR;    // + 4 scale loads for the group format
 };
 
-template <int ACT, int WF, int EPI, int WAVES, bool SK>
+// TN: block tile width in n, 256 or 192 (the 192-wide tile fills a wave of workgroups where 256 would leave a
+// quarter of the CUs idle, e.g. 4096 x 3072 outputs: 16 x 16 tiles instead of 16 x 12). The waves' n extent
+// is TN / 2 = JB blocks of 32.
+template <int ACT, int WF, int EPI, int WAVES, bool SK, int TN = BN>
 __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
   using C_ = Cfg<WAVES>;
+  static_assert(TN == BN || (TN == 192 && !SK && EPI != KH_EPI_SWIGLU), "192-wide tiles: data-parallel, no SwiGLU");
+  constexpr int JB = TN / 64, WN = TN / 2;
   constexpr int NTHR = C_::NTHR, IB = C_::IB, X_LOADS = C_::X_LOADS, KR = C_::KR, WCH = C_::WCH;
   // [X stage 0 | X stage 1 | X stage 2 | W stage 0 | W stage 1], 32 KB each
   __shared__ __attribute__((aligned(1024))) char lds[(X_STAGES + W_STAGES) * STAGE];
@@ -178,7 +184,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
   // ---- work of this workgroup: a range of K steps over the tile sequence. Data-parallel: one whole tile.
   //      Stream-K (sk_iters > 0): sk_iters steps starting at (cta * sk_iters), crossing tile boundaries;
   //      cta ids are made contiguous per XCD so one XCD's workgroups walk neighbouring tiles. ----
-  const int tiles_n = (p.N + BN - 1) / BN, tiles_m = (p.M + BM - 1) / BM;
+  const int tiles_n = (p.N + TN - 1) / TN, tiles_m = (p.M + BM - 1) / BM;
   const int total = tiles_n * tiles_m;
   const int nk = p.K / BK;
   int cta = blockIdx.x, it, it_end;
@@ -199,7 +205,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
     const int gm = min(GROUP_M, tiles_m - first_m);
     const int in_g = tile % group_sz;
     m0 = (first_m + in_g % gm) * BM;
-    n0 = (in_g / gm) * BN;
+    n0 = (in_g / gm) * TN;
   };
 
   // ---- X tile (activations) -> LDS directly: instruction r of wave w fills 1 KB block b = WAVES r + w,
@@ -217,7 +223,9 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
                                        (lds_void*)(dst + r * WAVES * 1024), 16, 0, 0);
   };
 
-  // ---- W tile: wave w loads k-rows [KR w, KR w + KR), lane columns n0 + 4 lane .. + 3 ----
+  // ---- W tile: wave w loads k-rows [KR w, KR w + KR), lane columns n0 + 4 wl .. + 3. With TN = 192, lanes
+  //      48..63 repeat lanes 32..47 (same loads, same LDS writes of the same values) ----
+  const int wl = (TN == 256 || lane < TN / 4) ? lane : lane - 16;
   constexpr int WB = (WF == WF_16) ? 2 : 1;
   int wcol = 0;  // columns >= N (last tile) are loaded clamped and never stored
   const char* wbase = nullptr;
@@ -225,7 +233,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
   auto set_operands = [&]() {
 #pragma unroll
     for (int r = 0; r < X_LOADS; r++) xoff[r] = min(m0 + 8 * WAVES * r + xrow0, p.M - 1) * p.lda + xchunk;
-    wcol = min(n0 + lane * 4, p.N - 4);
+    wcol = min(n0 + wl * 4, p.N - 4);
     wbase = (const char*)p.W + ((size_t)(wave * KR) * p.ldw + wcol) * WB;
   };
   // untracked loads (see vm_load_b32): their waits are the explicit vmcnt of step() / the prologue
@@ -266,7 +274,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
   for (int j = 0; j < 4; j++)
 #pragma unroll
     for (int h = 0; h < H; h++) {
-      const int nl = lane * 4 + j;
+      const int nl = wl * 4 + j;
       woff[j * H + h] = nl * 128 + (((H * wave + h) ^ swz(nl)) * 16);
     }
   auto store_w = [&](const WRaw<WF, KR>& R, int stage, int q) {  // quarter q of the thread's chunks
@@ -276,19 +284,19 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
       *(u32x4*)(base + woff[c]) = convert_chunk<ACT, WF, KR>(R, c / H, c % H);
   };
 
-  // ---- MFMA operands: wave (wn, wm) owns n [128 wn, +128) x m [WME wm, +WME) = 4 x IB blocks of 32 x 32 ----
+  // ---- MFMA operands: wave (wn, wm) owns n [WN wn, +WN) x m [WME wm, +WME) = JB x IB blocks of 32 x 32 ----
   const int wn = wave & 1, wm = wave >> 1;
   const int l32 = lane & 31, khalf = lane >> 5;
-  const int w_rd = (wn * 128 + l32) * 128, x_rd = (wm * C_::WME + l32) * 128;
+  const int w_rd = (wn * WN + l32) * 128, x_rd = (wm * C_::WME + l32) * 128;
   int sw[4];
 #pragma unroll
   for (int s = 0; s < 4; s++) sw[s] = (((2 * s + khalf) ^ swz(l32)) * 16);
 
-  f32x16 acc[4][IB];
+  f32x16 acc[JB][IB];
 
-  auto read_frags = [&](const char* xs, const char* ws, int s, u32x4 (&wf)[4], u32x4 (&xf)[IB]) {
+  auto read_frags = [&](const char* xs, const char* ws, int s, u32x4 (&wf)[JB], u32x4 (&xf)[IB]) {
 #pragma unroll
-    for (int jb = 0; jb < 4; jb++) wf[jb] = *(const u32x4*)(ws + w_rd + jb * 32 * 128 + sw[s]);
+    for (int jb = 0; jb < JB; jb++) wf[jb] = *(const u32x4*)(ws + w_rd + jb * 32 * 128 + sw[s]);
 #pragma unroll
     for (int ib = 0; ib < IB; ib++) xf[ib] = *(const u32x4*)(xs + x_rd + ib * 32 * 128 + sw[s]);
   };
@@ -309,7 +317,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
     ready_w(Rc, NewerT{});
     const char* xs = lds + (t % X_STAGES) * STAGE;
     const char* ws = lds + (X_STAGES + (t & 1)) * STAGE;
-    u32x4 wf[2][4], xf[2][IB];
+    u32x4 wf[2][JB], xf[2][IB];
     read_frags(xs, ws, 0, wf[0], xf[0]);
 #pragma unroll
     for (int s = 0; s < 4; s++) {
@@ -319,7 +327,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
       if (s < 3) read_frags(xs, ws, s + 1, wf[(s + 1) & 1], xf[(s + 1) & 1]);
       SCHED_FENCE();
 #pragma unroll
-      for (int jb = 0; jb < 4; jb++)
+      for (int jb = 0; jb < JB; jb++)
 #pragma unroll
         for (int ib = 0; ib < IB; ib++) acc[jb][ib] = mfma32<ACT>(wf[s & 1][jb], xf[s & 1][ib], acc[jb][ib]);
       store_w(Rc, (t + 1) & 1, s);
@@ -342,7 +350,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
   }
   first_seg = false;
 #pragma unroll
-  for (int jb = 0; jb < 4; jb++)
+  for (int jb = 0; jb < JB; jb++)
 #pragma unroll
     for (int ib = 0; ib < IB; ib++) acc[jb][ib] = (f32x16){};
 
@@ -371,7 +379,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
   // ---- stream-K: a tile split over workgroups c0..c1 (K order). Each stores its partial accumulators to
   //      its workspace slot and counts itself in; the last to arrive adds all partials in c0..c1 order
   //      (deterministic whatever the arrival order) and runs the epilogue. No workgroup ever waits. ----
-  if (SK && ns != nk) {
+  if constexpr (SK) if (ns != nk) {
     const int c0 = (tile * nk) / p.sk_iters, c1 = (tile * nk + nk - 1) / p.sk_iters;
     // a workgroup has at most two split tiles: slot 2c for its first tile, 2c + 1 for its last
     auto slot = [&](int c) {
@@ -430,18 +438,18 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
   //      are staged as f32, then the finished values are staged row-major and written out (or, for the
   //      residual epilogues, read-modify-written) with 16-byte vectors covering whole rows of the tile.
   //      Per (jb, ib) the lane holds row m = WME wm + 32 ib + l32 and columns
-  //      n = 128 wn + 32 jb + 8 g + 4 khalf + e (g, e = 0..3) of the tile in acc[jb][ib][4 g + e]. ----
+  //      n = WN wn + 32 jb + 8 g + 4 khalf + e (g, e = 0..3) of the tile in acc[jb][ib][4 g + e]. ----
   constexpr bool OUT16 = (EPI == KH_EPI_STORE16 || EPI == KH_EPI_GELU || EPI == KH_EPI_BIAS16 || EPI == KH_EPI_SWIGLU);
   constexpr bool HAS_VEC = (EPI == KH_EPI_RESID_GATE || EPI == KH_EPI_BIAS16 || EPI == KH_EPI_BIAS_F32);
-  constexpr int OUT_COLS = (EPI == KH_EPI_SWIGLU) ? BN / 2 : BN;
+  constexpr int OUT_COLS = (EPI == KH_EPI_SWIGLU) ? TN / 2 : TN;
   constexpr int ELEM = OUT16 ? 2 : 4;
   constexpr int ROW_BYTES = OUT_COLS * ELEM + 16;             // padded staging row
   constexpr int PASS_ROWS = OUT16 ? BM : BM / 2;              // f32 tiles go out in two row halves
   constexpr int SC_OFF = PASS_ROWS * ROW_BYTES;
-  static_assert(SC_OFF + 2 * BN * 4 <= (X_STAGES + W_STAGES) * STAGE, "epilogue staging exceeds LDS");
+  static_assert(SC_OFF + 2 * TN * 4 <= (X_STAGES + W_STAGES) * STAGE, "epilogue staging exceeds LDS");
   float* sc_l = (float*)(lds + SC_OFF);
-  float* vv_l = sc_l + BN;
-  if (tid < BN) {
+  float* vv_l = sc_l + TN;
+  if (tid < TN) {
     const int n = n0 + tid;
     float sv = 1.f, vv = 0.f;
     if (n < p.N) {
@@ -460,11 +468,11 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
     if (PASS_ROWS == BM || (wm * C_::WME) / PASS_ROWS == pass) {
       const int row_base = wm * C_::WME - pass * PASS_ROWS;
 #pragma unroll
-      for (int jb = 0; jb < 4; jb++) {
+      for (int jb = 0; jb < JB; jb++) {
         if (EPI == KH_EPI_SWIGLU && (jb & 1)) continue;  // up blocks are consumed with their gate block
 #pragma unroll
         for (int g = 0; g < 4; g++) {
-          const int nl = wn * 128 + jb * 32 + g * 8 + khalf * 4;  // tile column of e = 0
+          const int nl = wn * WN + jb * 32 + g * 8 + khalf * 4;  // tile column of e = 0
           const f32x4 sc = *(const f32x4*)(sc_l + nl);
           f32x4 sc_up = sc, vv = {};
           if (EPI == KH_EPI_SWIGLU) sc_up = *(const f32x4*)(sc_l + nl + 32);
@@ -521,15 +529,18 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
 }
 
 template <int ACT, int WF>
-hipError_t launch_epi(int epi, const GemmArgs& a, int grid_x, hipStream_t st) {
+hipError_t launch_epi(int epi, const GemmArgs& a, int grid_x, int tn, hipStream_t st) {
   dim3 grid(grid_x), block(64 * WAVES_DEFAULT);
   switch (epi) {
-#define KH_CASE(E)                                                                          \
-  case E:                                                                                   \
-    if (a.sk_iters > 0)                                                                     \
-      hipLaunchKernelGGL((gemm_kernel<ACT, WF, E, WAVES_DEFAULT, true>), grid, block, 0, st, a);  \
-    else                                                                                    \
-      hipLaunchKernelGGL((gemm_kernel<ACT, WF, E, WAVES_DEFAULT, false>), grid, block, 0, st, a); \
+#define KH_CASE(E)                                                                                    \
+  case E:                                                                                             \
+    if (a.sk_iters > 0)                                                                               \
+      hipLaunchKernelGGL((gemm_kernel<ACT, WF, E, WAVES_DEFAULT, true>), grid, block, 0, st, a);     \
+    else if (E != KH_EPI_SWIGLU && tn == 192)                                                         \
+      hipLaunchKernelGGL((gemm_kernel<ACT, WF, E, WAVES_DEFAULT, false, (E == KH_EPI_SWIGLU ? BN : 192)>), \
+                         grid, block, 0, st, a);                                                      \
+    else                                                                                              \
+      hipLaunchKernelGGL((gemm_kernel<ACT, WF, E, WAVES_DEFAULT, false>), grid, block, 0, st, a);    \
     break;
     KH_CASE(KH_EPI_STORE16)
     KH_CASE(KH_EPI_F32)
@@ -547,12 +558,12 @@ hipError_t launch_epi(int epi, const GemmArgs& a, int grid_x, hipStream_t st) {
 }
 
 template <int ACT>
-hipError_t launch_wf(int wf, int epi, const GemmArgs& a, int g, hipStream_t st) {
-  if (wf == WF_16) return launch_epi<ACT, WF_16>(epi, a, g, st);
-  if (wf == WF_I8_CHANNEL) return launch_epi<ACT, WF_I8_CHANNEL>(epi, a, g, st);
-  if (wf == WF_I8_GROUP) return launch_epi<ACT, WF_I8_GROUP>(epi, a, g, st);
-  if (wf == WF_I8_GROUP_F16) return launch_epi<ACT, WF_I8_GROUP_F16>(epi, a, g, st);
-  return launch_epi<ACT, WF_I8_GROUP_BF16>(epi, a, g, st);
+hipError_t launch_wf(int wf, int epi, const GemmArgs& a, int g, int tn, hipStream_t st) {
+  if (wf == WF_16) return launch_epi<ACT, WF_16>(epi, a, g, tn, st);
+  if (wf == WF_I8_CHANNEL) return launch_epi<ACT, WF_I8_CHANNEL>(epi, a, g, tn, st);
+  if (wf == WF_I8_GROUP) return launch_epi<ACT, WF_I8_GROUP>(epi, a, g, tn, st);
+  if (wf == WF_I8_GROUP_F16) return launch_epi<ACT, WF_I8_GROUP_F16>(epi, a, g, tn, st);
+  return launch_epi<ACT, WF_I8_GROUP_BF16>(epi, a, g, tn, st);
 }
 
 // ---- stream-K workspace: per (device, stream), allocated on first use and kept until the process ends.
@@ -613,35 +624,54 @@ const SkWorkspace* sk_workspace(int dev, hipStream_t st, int ctas) {
   return w.ws ? &sk_map[key] : nullptr;
 }
 
+// KH_GEMM_TN192=0 keeps every data-parallel launch on 256-wide tiles (read per call)
+bool tn192_enabled() {
+  const char* e = getenv("KH_GEMM_TN192");
+  return !(e && e[0] == '0');
+}
+
 // Data-parallel (one tile per workgroup) unless the tiles fill the last wave of workgroups poorly; then
 // stream-K spreads the tiles' K steps evenly over one wave of workgroups.
-void plan_launch(GemmArgs& a, hipStream_t st, int& grid_x) {
-  const int tiles = ((a.N + BN - 1) / BN) * ((a.M + BM - 1) / BM);
+void plan_launch(GemmArgs& a, int epi, hipStream_t st, int& grid_x, int& tn) {
+  const int tiles_m = (a.M + BM - 1) / BM;
+  const int tiles = ((a.N + BN - 1) / BN) * tiles_m;
   const int nk = a.K / BK;
   grid_x = tiles;
+  tn = BN;
   a.sk_iters = 0;
   a.ws = nullptr;
   a.cnt = nullptr;
-  if (!sk_enabled() || tiles > SK_MAX_TILES) return;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return;
   const int ctas = sk_cta_count(dev);
   if (ctas <= 0) return;
+  const int rounds = (tiles + ctas - 1) / ctas;
   // Stream-K staggers the workgroups' K offsets, so neighbouring tiles no longer share X / W panels in L2
   // at the same time: measured, it loses to data-parallel launches that fill >= 75 % of their last wave
   // (4608 x 3072 x 3072: 140 vs 103 us) and wins where most CUs would idle (1536 x 3072 x 12288: 156 vs
   // 303 us). It is used below 60 % occupancy.
-  const int rounds = (tiles + ctas - 1) / ctas;
-  if ((double)tiles / ((double)rounds * ctas) >= 0.6) return;
-  const long long iters = (long long)tiles * nk;
-  const int per = (int)((iters + ctas - 1) / ctas);
-  if (per < SK_MIN_ITERS) return;
-  const SkWorkspace* w = sk_workspace(dev, st, ctas);
-  if (!w) return;
-  a.sk_iters = per;
-  a.ws = w->ws;
-  a.cnt = w->cnt;
-  grid_x = ctas;
+  if (sk_enabled() && tiles <= SK_MAX_TILES && (double)tiles / ((double)rounds * ctas) < 0.6) {
+    const long long iters = (long long)tiles * nk;
+    const int per = (int)((iters + ctas - 1) / ctas);
+    const SkWorkspace* w = per >= SK_MIN_ITERS ? sk_workspace(dev, st, ctas) : nullptr;
+    if (w) {
+      a.sk_iters = per;
+      a.ws = w->ws;
+      a.cnt = w->cnt;
+      grid_x = ctas;
+      return;
+    }
+  }
+  // 192-wide tiles where 256-wide ones leave part of a single wave of workgroups idle and 192-wide ones still
+  // fit in one wave (4096 x 3072 outputs: 256 tiles instead of 192; measured 349 -> 326 us at K = 12288).
+  // Not where they add a partial wave: at 4608 x 12288 (864 vs 1152 tiles) they measured 390 -> 410 us.
+  if (epi != KH_EPI_SWIGLU && a.N % 192 == 0 && tn192_enabled() && tiles < ctas) {
+    const int tiles192 = (a.N / 192) * tiles_m;
+    if (tiles192 > tiles && tiles192 <= ctas) {
+      tn = 192;
+      grid_x = tiles192;
+    }
+  }
 }
 
 }  // namespace
@@ -687,10 +717,10 @@ int gemm(hipStream_t st, int epi, const void* A, int a_dtype, const kh_weight& W
   int gshift = 0;  // log2(group / BK): K step t reads scale row t >> gshift
   while ((BK << gshift) < group) gshift++;
   GemmArgs a{A, W.w, W.s, C, (const float*)vec, M, N, K, lda, ldw, ldc, gshift, W.s_dtype, 0, nullptr, nullptr};
-  int grid_x = 0;
-  plan_launch(a, st, grid_x);
-  hipError_t r = a_dtype == KH_F16 ? launch_wf<KH_F16>(wf, epi, a, grid_x, st)
-                                   : launch_wf<KH_BF16>(wf, epi, a, grid_x, st);
+  int grid_x = 0, tn = BN;
+  plan_launch(a, epi, st, grid_x, tn);
+  hipError_t r = a_dtype == KH_F16 ? launch_wf<KH_F16>(wf, epi, a, grid_x, tn, st)
+                                   : launch_wf<KH_BF16>(wf, epi, a, grid_x, tn, st);
   if (r != hipSuccess) return e.hip(r, "gemm launch");
   return KH_OK;
 }
