@@ -107,9 +107,8 @@ __device__ __forceinline__ int vt_off(int d, int kq) {
 
 template <int DT, bool GATE, bool BIG, bool CAUSAL>
 __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
-  // [K stage 0 | K stage 1 | V^T stage 0 | 1 | 2] (+ the fp32 rank-1 key terms of two blocks when BIG)
-  __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES + (BIG ? 2 * BKEYS * 4 : 0)];
-  float* const kb_s = (float*)(lds + LDS_BYTES);  // [2][BKEYS], BIG only
+  // [K stage 0 | K stage 1 | V^T stage 0 | 1 | 2]
+  __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];
   typedef __attribute__((address_space(3))) void lds_void;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -132,7 +131,11 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
 #pragma unroll
     for (int s = 0; s < 8; s++) qf[s] = *(const u32x4*)(qp + s * 16);
   }
-  const float qb = BIG ? p.QB[(size_t)qc * p.ldqb + h] : 0.f;
+  // rank-1 fp32 term qb[q] kb[k] (BIG): the initial accumulator of each 32-key S^T block is the outer
+  // product kb qb^T, one v_mfma_f32_32x32x2_f32 with A = kb (key rows, k-slice 0; the lanes of k-slice 1
+  // hold 0) and B = qb (query columns, likewise): it lands in the S^T accumulator layout, needs no LDS and
+  // keeps the workgroup at 80 KB (two per CU). The product is exact before the 16-bit products are added.
+  const float qb_op = (BIG && hh == 0) ? p.QB[(size_t)qc * p.ldqb + h] : 0.f;
 
   // key range of this workgroup (causal: up to its last query's visible key)
   int kend = p.Lk;
@@ -182,8 +185,13 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
       *(u32x2*)(vt + vt_off(d, vkq)) = (u32x2){lo, hi};
     }
   };
-  auto stage_kb = [&](int b, int buf) {
-    if (BIG && tid < BKEYS) kb_s[buf * BKEYS + tid] = p.KB[(size_t)min(b * BKEYS + tid, p.Lk - 1) * p.ldkb + kvh];
+  // kb of keys 32 kh + l32 of block b (lanes of k-slice 1 hold 0), loaded one block ahead
+  float kbv[2] = {0.f, 0.f};
+  auto load_kb = [&](int b) {
+    if (BIG && hh == 0) {
+#pragma unroll
+      for (int kh = 0; kh < 2; kh++) kbv[kh] = p.KB[(size_t)min(b * BKEYS + kh * 32 + l32, p.Lk - 1) * p.ldkb + kvh];
+    }
   };
 
   f32x16 o[4];
@@ -209,7 +217,7 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
   if (nblk > 0) {
     issue_k(0, 0);
     load_v(0);
-    stage_kb(0, 0);
+    load_kb(0);
     store_vt(0);
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
     lds_barrier();
@@ -225,7 +233,6 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
     if (has_next) {
       issue_k(b + 1, (b + 1) & 1);
       load_v(b + 1);
-      stage_kb(b + 1, (b + 1) & 1);
     }
     const char* kt = lds + (b & 1) * KT_BYTES;
 
@@ -233,7 +240,7 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
     f32x16 st[2];
 #pragma unroll
     for (int kh = 0; kh < 2; kh++) {
-      st[kh] = (f32x16){};
+      st[kh] = BIG ? __builtin_amdgcn_mfma_f32_32x32x2f32(kbv[kh], qb_op, (f32x16){}, 0, 0, 0) : (f32x16){};
       const int krow = kh * 32 + l32;
 #pragma unroll
       for (int s = 0; s < 8; s++) {
@@ -241,6 +248,7 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
         st[kh] = mfma32<DT>(kf, qf[s], st[kh]);
       }
     }
+    if (has_next) load_kb(b + 1);
     if (b > 0) pv(pf, (b - 1) % V_STAGES);
 
     // block max on the raw scores (the positive scale commutes with max); masked scores are -inf
@@ -250,7 +258,6 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
 #pragma unroll
       for (int i = 0; i < 16; i++) {
         float s = st[kh][i];
-        if constexpr (BIG) s += qb * kb_s[(b & 1) * BKEYS + kh * 32 + (i >> 2) * 8 + hh * 4 + (i & 3)];
         if constexpr (MASK) {
           const int key = b * BKEYS + kh * 32 + (i >> 2) * 8 + hh * 4 + (i & 3);
           if (key >= p.Lk || (CAUSAL && key > q + p.q_pos0)) s = -INFINITY;

@@ -66,6 +66,13 @@ def test_attention_big_term(dev):
     run(dev, O.BF16, 160, 200, 4, group=2, big=True, seed=5)
 
 
+@pytest.mark.parametrize("dtype,causal,gate", [(O.F16, 0, True), (O.BF16, 1, False), (O.BF16, 0, True)])
+def test_attention_big_term_many_blocks(dev, dtype, causal, gate):
+    """The rank-1 fp32 term over many key blocks (its per-block kb prefetch), ragged tails, GQA, with the
+    gate and the causal mask."""
+    run(dev, dtype, 700, 700, 4, group=2, causal=causal, gate=gate, big=True, seed=8 + causal)
+
+
 def test_attention_peaky_scores(dev):
     """Large logits (scale 4 inputs) exercise the lazy max update and the rescale path."""
     run(dev, O.F16, 256, 512, 2, seed=6, scale=4.0)
