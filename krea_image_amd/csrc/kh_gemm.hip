@@ -65,7 +65,16 @@ struct GemmArgs {
   int sk_iters;  // stream-K: K steps per workgroup (0 = one tile per workgroup)
   float* ws;     // stream-K partial tiles: 2 slots of BM x BN f32 per workgroup
   int* cnt;      // stream-K arrival counts per tile (zero between launches)
+  // implicit 3 x 3 convolution (CONV kernels): A is an NHWC image [pixels, lda] of cv_C channels, the GEMM
+  // rows are the cv_H x cv_W output pixels and K runs over (tap, channel) (tools/convert.py:338-344);
+  // cv_up: the image is cv_H / 2 x cv_W / 2, nearest-upsampled. cv_cinv = ceil(2^32 / cv_C).
+  int cv_C, cv_H, cv_W, cv_up;
+  uint32_t cv_cinv;
 };
+
+// 16 zero bytes in device memory (never written): the source of the activation DMA for the taps of a
+// convolution that fall outside the image (zero padding) and for the K padding past 9 C.
+__device__ __attribute__((aligned(16))) uint32_t g_zero_chunk[4] = {0u, 0u, 0u, 0u};
 
 // 16-byte chunk XOR of LDS row `row` (rows are 128 bytes = 8 chunks of 8 k). Depends on row & 31 only, is a
 // bijection on any 8 consecutive rows (operand reads: 32 consecutive rows per instruction) and on rows
@@ -169,7 +178,8 @@ struct Cfg {
 // TN: block tile width in n, 256 or 192 (the 192-wide tile fills a wave of workgroups where 256 would leave a
 // quarter of the CUs idle, e.g. 4096 x 3072 outputs: 16 x 16 tiles instead of 16 x 12). The waves' n extent
 // is TN / 2 = JB blocks of 32.
-template <int ACT, int WF, int EPI, int WAVES, bool SK, int TN = BN>
+// CONV: the activation tile is gathered from an image as an implicit 3 x 3 convolution (GemmArgs cv_*).
+template <int ACT, int WF, int EPI, int WAVES, bool SK, int TN = BN, bool CONV = false>
 __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
   using C_ = Cfg<WAVES>;
   static_assert(TN == BN || (TN == 192 && !SK && EPI != KH_EPI_SWIGLU), "192-wide tiles: data-parallel, no SwiGLU");
@@ -214,13 +224,32 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
   const int xrow0 = wave * 8 + (lane >> 3);
   const int xchunk = ((lane & 7) ^ swz(xrow0)) * 8;
   int xoff[X_LOADS];
+  int cy[CONV ? X_LOADS : 1], cx[CONV ? X_LOADS : 1];  // CONV: output pixel (row, column) of each load's row
   const uint16_t* xbase = (const uint16_t*)p.A;
   auto issue_x_to = [&](int t, int stage) {
     char* dst = lds + stage * STAGE + wave * 1024;
+    if constexpr (CONV) {
+      // k = (tap, channel) of this lane's 8 columns (C % 8 == 0: never across two taps); taps outside the
+      // image and k >= 9 C read the zero chunk
+      const uint32_t k = (uint32_t)((kb + t) * BK + xchunk);
+      const int tap = (int)__umulhi(k, p.cv_cinv), ci = (int)k - tap * p.cv_C;
+      const int ty = (tap * 11) >> 5, dy = ty - 1, dx = tap - 3 * ty - 1;  // tap / 3 for tap < 12
+      const int win = p.cv_up ? p.cv_W >> 1 : p.cv_W;
 #pragma unroll
-    for (int r = 0; r < X_LOADS; r++)
-      __builtin_amdgcn_global_load_lds((const void*)(xbase + xoff[r] + (kb + t) * BK),
-                                       (lds_void*)(dst + r * WAVES * 1024), 16, 0, 0);
+      for (int r = 0; r < X_LOADS; r++) {
+        int sy = cy[r] + dy, sx = cx[r] + dx;
+        const bool in = tap < 9 && sy >= 0 && sy < p.cv_H && sx >= 0 && sx < p.cv_W;
+        sy >>= p.cv_up;
+        sx >>= p.cv_up;
+        const void* src = in ? (const void*)(xbase + ((size_t)sy * win + sx) * p.lda + ci) : (const void*)g_zero_chunk;
+        __builtin_amdgcn_global_load_lds(src, (lds_void*)(dst + r * WAVES * 1024), 16, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < X_LOADS; r++)
+        __builtin_amdgcn_global_load_lds((const void*)(xbase + xoff[r] + (kb + t) * BK),
+                                         (lds_void*)(dst + r * WAVES * 1024), 16, 0, 0);
+    }
   };
 
   // ---- W tile: wave w loads k-rows [KR w, KR w + KR), lane columns n0 + 4 wl .. + 3. With TN = 192, lanes
@@ -232,7 +261,15 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
   const size_t wrow = (size_t)p.ldw * WB;
   auto set_operands = [&]() {
 #pragma unroll
-    for (int r = 0; r < X_LOADS; r++) xoff[r] = min(m0 + 8 * WAVES * r + xrow0, p.M - 1) * p.lda + xchunk;
+    for (int r = 0; r < X_LOADS; r++) {
+      const int m = min(m0 + 8 * WAVES * r + xrow0, p.M - 1);
+      if constexpr (CONV) {
+        cy[r] = m / p.cv_W;
+        cx[r] = m - cy[r] * p.cv_W;
+      } else {
+        xoff[r] = m * p.lda + xchunk;
+      }
+    }
     wcol = min(n0 + wl * 4, p.N - 4);
     wbase = (const char*)p.W + ((size_t)(wave * KR) * p.ldw + wcol) * WB;
   };
@@ -566,6 +603,18 @@ hipError_t launch_wf(int wf, int epi, const GemmArgs& a, int g, int tn, hipStrea
   return launch_epi<ACT, WF_I8_GROUP_BF16>(epi, a, g, tn, st);
 }
 
+template <int ACT>
+hipError_t launch_conv(const GemmArgs& a, int grid_x, int tn, hipStream_t st) {
+  dim3 grid(grid_x), block(64 * WAVES_DEFAULT);
+  if (a.sk_iters > 0)
+    hipLaunchKernelGGL((gemm_kernel<ACT, WF_16, KH_EPI_BIAS16, WAVES_DEFAULT, true, BN, true>), grid, block, 0, st, a);
+  else if (tn == 192)
+    hipLaunchKernelGGL((gemm_kernel<ACT, WF_16, KH_EPI_BIAS16, WAVES_DEFAULT, false, 192, true>), grid, block, 0, st, a);
+  else
+    hipLaunchKernelGGL((gemm_kernel<ACT, WF_16, KH_EPI_BIAS16, WAVES_DEFAULT, false, BN, true>), grid, block, 0, st, a);
+  return hipGetLastError();
+}
+
 // ---- stream-K workspace: per (device, stream), allocated on first use and kept until the process ends.
 //      Launches on one stream are ordered, so one workspace per stream is race-free. ----
 constexpr int SK_MAX_TILES = 1 << 16;
@@ -722,6 +771,33 @@ int gemm(hipStream_t st, int epi, const void* A, int a_dtype, const kh_weight& W
   hipError_t r = a_dtype == KH_F16 ? launch_wf<KH_F16>(wf, epi, a, grid_x, tn, st)
                                    : launch_wf<KH_BF16>(wf, epi, a, grid_x, tn, st);
   if (r != hipSuccess) return e.hip(r, "gemm launch");
+  return KH_OK;
+}
+
+}  // namespace kh
+
+namespace kh {
+
+int conv3x3(hipStream_t st, const void* x, int ldx, int C, int H, int W, int up, int dtype, const kh_weight& Wt, int K,
+            int N, const float* bias, void* y, int ldy, Err& e) {
+  if (dtype != KH_F16 && dtype != KH_BF16) return e.fail("conv3x3: dtype must be f16 or bf16");
+  if (!x || !Wt.w || !y || !bias) return e.fail("conv3x3: null x / W / bias / y");
+  if (Wt.w_dtype != dtype) return e.fail("conv3x3: weights must be 16-bit of the activation type");
+  if (H <= 0 || W <= 0 || C <= 0 || N <= 0) return e.fail("conv3x3: empty shape H=%d W=%d C=%d N=%d", H, W, C, N);
+  if (C % 8) return e.fail("conv3x3: C=%d must be a multiple of 8", C);
+  if (ldx < C || ldx % 8) return e.fail("conv3x3: ldx=%d must be >= C and a multiple of 8", ldx);
+  if (up && (H % 2 || W % 2)) return e.fail("conv3x3: upsampling needs an even output size (%d x %d)", H, W);
+  if (K % BK || K < 9 * C) return e.fail("conv3x3: K=%d must be a multiple of 64 and >= 9 C = %d", K, 9 * C);
+  if (N % 64) return e.fail("conv3x3: N=%d must be a multiple of 64", N);
+  if (ldy < N || ldy % 8) return e.fail("conv3x3: ldy=%d must be >= N and a multiple of 8", ldy);
+  if ((long long)H * W >= (1LL << 31)) return e.fail("conv3x3: too many pixels");
+  if (((uintptr_t)x | (uintptr_t)Wt.w | (uintptr_t)y) & 15) return e.fail("conv3x3: x, W and y must be 16-byte aligned");
+  GemmArgs a{x, Wt.w, nullptr, y, bias, H * W, N, K, ldx, N, ldy, 0, KH_F32, 0, nullptr, nullptr,
+             C, H, W, up ? 1 : 0, (uint32_t)((((uint64_t)1 << 32) + (uint64_t)C - 1) / (uint64_t)C)};
+  int grid_x = 0, tn = BN;
+  plan_launch(a, KH_EPI_BIAS16, st, grid_x, tn);
+  const hipError_t r = dtype == KH_F16 ? launch_conv<KH_F16>(a, grid_x, tn, st) : launch_conv<KH_BF16>(a, grid_x, tn, st);
+  if (r != hipSuccess) return e.hip(r, "conv3x3 launch");
   return KH_OK;
 }
 

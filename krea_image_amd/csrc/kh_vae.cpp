@@ -23,9 +23,8 @@ inline int ld_of(int C) { return (int)ru(C, 64); }  // GEMM outputs are padded t
 
 struct Plan {
   long long P0, P3, Pp0;  // VAE-input pixels, output pixels, P0 rounded up to 64
-  long long mc;           // im2col pixel chunk
-  size_t act, col, wpad, bpad, qkv, kt, S, Pm, total;
-  size_t off_act[5], off_col, off_wpad, off_bpad, off_qkv, off_kt, off_S, off_Pm;
+  size_t act, wpad, bpad, qkv, kt, S, Pm, total;
+  size_t off_act[5], off_wpad, off_bpad, off_qkv, off_kt, off_S, off_Pm;
 };
 
 Plan plan(int H16, int W16) {
@@ -36,8 +35,6 @@ Plan plan(int H16, int W16) {
   // largest activation: P x padded channels over the stages (P0 x 384, 4 P0 x 384, 16 P0 x 192, 64 P0 x 128)
   const long long a = std::max({p.P0 * MID_C, 4 * p.P0 * 384, 16 * p.P0 * ld_of(192), p.P3 * ld_of(96)});
   p.act = (size_t)ru(a * 2, 256);
-  p.mc = std::min<long long>(65536, p.P3);
-  p.col = (size_t)ru(p.mc * 9 * 384 * 2, 256);
   p.wpad = (size_t)ru(9LL * 384 * 384 * 2, 256);
   p.bpad = (size_t)ru(1152 * 4, 256);
   p.qkv = (size_t)ru(p.Pp0 * 3 * MID_C * 2, 256);
@@ -50,7 +47,6 @@ Plan plan(int H16, int W16) {
     p.off_act[i] = off;
     off += p.act;
   }
-  p.off_col = off, off += p.col;
   p.off_wpad = off, off += p.wpad;
   p.off_bpad = off, off += p.bpad;
   p.off_qkv = off, off += p.qkv;
@@ -132,16 +128,9 @@ class Decoder {
     }
     const int H = up ? 2 * x.H : x.H, Wd = up ? 2 * x.W : x.W;
     if ((rc = acquire(H, Wd, cout, Np, y))) return rc;
-    uint16_t* col = (uint16_t*)(ws_ + pl_.off_col);
-    const long long P = (long long)H * Wd;
-    const long long mc = std::max<long long>(1, std::min<long long>(pl_.mc, (long long)(pl_.col / ((size_t)Kp * 2))));
     const kh_weight wt{W, nullptr, KH_BF16, KH_F32, 0};
-    for (long long m0 = 0; m0 < P; m0 += mc) {
-      const int rows = (int)std::min(mc, P - m0);
-      if ((rc = vae_im2col(st_, x.p, x.ld, x.C, H, Wd, up, (int)m0, rows, col, Kp, e_))) return rc;
-      if ((rc = gemm(st_, KH_EPI_BIAS16, col, KH_BF16, wt, y.p + (size_t)m0 * Np, rows, Np, Kp, Kp, Np, Np, bias, e_)))
-        return rc;
-    }
+    if ((rc = kh::conv3x3(st_, x.p, x.ld, x.C, H, Wd, up, KH_BF16, wt, Kp, Np, bias, y.p, Np, e_))) return rc;
+    const long long P = (long long)H * Wd;
     if (res) {
       if (res->ld != y.ld || res->P() != P) return e_.fail("vae: residual shape mismatch");
       if ((rc = vae_add(st_, y.p, res->p, P * y.ld, e_))) return rc;

@@ -5,11 +5,12 @@
 // Activations are NHWC bf16 rows [pixel, channel] with a row stride; weights are the converter's
 // implicit-GEMM layout Wt[(ky * 3 + kx) * Cin + ci, co] (tools/convert.py:338-344).
 //
-// Design: every convolution with a real channel count runs on the dequant-GEMM core (kh_gemm, 16-bit
-// weights): the 3 x 3 (optionally nearest-2x-upsampled) input is expanded into an im2col panel
-// [pixels, 9 Cin] in HBM, in pixel chunks, and multiplied by the weights with the bias epilogue. These
-// kernels are the memory-bound steps around it: im2col, the channel RMS norm, the residual add, the
-// latent unpack, the mid-block attention's K transpose and row softmax, and the 4-channel output conv.
+// Design: every convolution with a real channel count runs on the GEMM core (16-bit weights, bias
+// epilogue): 3 x 3 convs (optionally nearest-2x-upsampled) as an implicit GEMM whose activation DMA
+// gathers each (tap, channel) chunk straight from the image (conv3x3 in kh_gemm.hip), 1 x 1 convs as a
+// plain GEMM. These kernels are the memory-bound steps around it: the channel RMS norm, the residual add,
+// the latent unpack, the mid-block attention's K transpose and row softmax, the 4-channel output conv, and
+// an explicit im2col (kept as an exported op: the reference the implicit loader is tested against).
 #include "kh_common.h"
 #include "kh_internal.h"
 
