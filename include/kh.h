@@ -66,10 +66,11 @@ typedef struct kh_weight {
  * steps spread over one workgroup per CU); those launches use a workspace of 2 x CUs x 256 KiB + 256 KiB
  * that kh_gemm allocates once per (device, stream) on first need and keeps until the process ends (on a
  * capturing stream without one, the launch stays data-parallel). Results are deterministic either way.
- * KH_GEMM_STREAMK=0 in the environment keeps every launch data-parallel. A data-parallel launch whose 256 x 256
- * tiles fill only part of one wave of workgroups uses 256 x 192 tiles when N % 192 == 0 and they still fit in
- * one wave (not for SWIGLU); KH_GEMM_TN192=0 keeps 256-wide tiles. Either tile sums each output's products in
- * the same order, so the results are bitwise identical.
+ * KH_GEMM_STREAMK=0 in the environment keeps every launch data-parallel. Data-parallel launches may use
+ * narrower tiles (not for SWIGLU): 256 x 192 where N pads less to 192 than to 256 (e.g. 384) or where
+ * 256-wide tiles fill only part of one wave of workgroups and 192-wide ones still fit in one (4096 x 3072);
+ * 256 x 128 for 16-bit weights where N pads less to 128 (e.g. 64, 128). KH_GEMM_TN192=0 keeps 256-wide
+ * tiles. Every tile width sums each output's products in the same order: the results are bitwise equal.
  * Replaces krea::Metal::gemm (engine/src/metal.h:66-69, engine/src/metal.mm:146-163). */
 int kh_gemm(kh_stream stream, int epi, const void* A, int a_dtype, const kh_weight* W, void* C, int M, int N, int K,
             int lda, int ldw, int ldc, const void* vec, char* err, int errlen);

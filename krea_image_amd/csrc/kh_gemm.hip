@@ -175,14 +175,15 @@ struct Cfg {
   static constexpr int LOADS = X_LOADS + KR;    // + 4 scale loads for the group format
 };
 
-// TN: block tile width in n, 256 or 192 (the 192-wide tile fills a wave of workgroups where 256 would leave a
-// quarter of the CUs idle, e.g. 4096 x 3072 outputs: 16 x 16 tiles instead of 16 x 12). The waves' n extent
-// is TN / 2 = JB blocks of 32.
+// TN: block tile width in n, 256, 192 or 128 (narrow tiles serve N that 256 would pad, e.g. 96 or 384
+// channels, and fill a wave of workgroups where 256 would leave CUs idle, e.g. 4096 x 3072 outputs: 16 x 16
+// tiles of 192 instead of 16 x 12). The waves' n extent is TN / 2 = JB blocks of 32.
 // CONV: the activation tile is gathered from an image as an implicit 3 x 3 convolution (GemmArgs cv_*).
 template <int ACT, int WF, int EPI, int WAVES, bool SK, int TN = BN, bool CONV = false>
 __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
   using C_ = Cfg<WAVES>;
-  static_assert(TN == BN || (TN == 192 && !SK && EPI != KH_EPI_SWIGLU), "192-wide tiles: data-parallel, no SwiGLU");
+  static_assert(TN == BN || ((TN == 192 || TN == 128) && !SK && EPI != KH_EPI_SWIGLU),
+                "narrow tiles (192 / 128): data-parallel, no SwiGLU");
   constexpr int JB = TN / 64, WN = TN / 2;
   constexpr int NTHR = C_::NTHR, IB = C_::IB, X_LOADS = C_::X_LOADS, KR = C_::KR, WCH = C_::WCH;
   // [X stage 0 | X stage 1 | X stage 2 | W stage 0 | W stage 1], 32 KB each
@@ -253,8 +254,9 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
   };
 
   // ---- W tile: wave w loads k-rows [KR w, KR w + KR), lane columns n0 + 4 wl .. + 3. With TN = 192, lanes
-  //      48..63 repeat lanes 32..47 (same loads, same LDS writes of the same values) ----
-  const int wl = (TN == 256 || lane < TN / 4) ? lane : lane - 16;
+  //      48..63 repeat lanes 32..47, with TN = 128 lanes 32..63 repeat 0..31 (same loads, same LDS writes of
+  //      the same values) ----
+  const int wl = (TN == 256 || lane < TN / 4) ? lane : lane - (64 - TN / 4);
   constexpr int WB = (WF == WF_16) ? 2 : 1;
   int wcol = 0;  // columns >= N (last tile) are loaded clamped and never stored
   const char* wbase = nullptr;
@@ -565,31 +567,40 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
   }  // segments
 }
 
+template <int ACT, int WF, int E, bool CONV = false>
+void launch_one(const GemmArgs& a, int grid_x, int tn, hipStream_t st) {
+  const dim3 grid(grid_x), block(64 * WAVES_DEFAULT);
+  if (a.sk_iters > 0) {
+    hipLaunchKernelGGL((gemm_kernel<ACT, WF, E, WAVES_DEFAULT, true, BN, CONV>), grid, block, 0, st, a);
+    return;
+  }
+  if constexpr (E != KH_EPI_SWIGLU) {
+    if (tn == 192) {
+      hipLaunchKernelGGL((gemm_kernel<ACT, WF, E, WAVES_DEFAULT, false, 192, CONV>), grid, block, 0, st, a);
+      return;
+    }
+    if constexpr (WF == WF_16) {  // 128-wide tiles: 16-bit weights only (the VAE's narrow channel counts)
+      if (tn == 128) {
+        hipLaunchKernelGGL((gemm_kernel<ACT, WF, E, WAVES_DEFAULT, false, 128, CONV>), grid, block, 0, st, a);
+        return;
+      }
+    }
+  }
+  hipLaunchKernelGGL((gemm_kernel<ACT, WF, E, WAVES_DEFAULT, false, BN, CONV>), grid, block, 0, st, a);
+}
+
 template <int ACT, int WF>
 hipError_t launch_epi(int epi, const GemmArgs& a, int grid_x, int tn, hipStream_t st) {
-  dim3 grid(grid_x), block(64 * WAVES_DEFAULT);
   switch (epi) {
-#define KH_CASE(E)                                                                                    \
-  case E:                                                                                             \
-    if (a.sk_iters > 0)                                                                               \
-      hipLaunchKernelGGL((gemm_kernel<ACT, WF, E, WAVES_DEFAULT, true>), grid, block, 0, st, a);     \
-    else if (E != KH_EPI_SWIGLU && tn == 192)                                                         \
-      hipLaunchKernelGGL((gemm_kernel<ACT, WF, E, WAVES_DEFAULT, false, (E == KH_EPI_SWIGLU ? BN : 192)>), \
-                         grid, block, 0, st, a);                                                      \
-    else                                                                                              \
-      hipLaunchKernelGGL((gemm_kernel<ACT, WF, E, WAVES_DEFAULT, false>), grid, block, 0, st, a);    \
-    break;
-    KH_CASE(KH_EPI_STORE16)
-    KH_CASE(KH_EPI_F32)
-    KH_CASE(KH_EPI_RESID_GATE)
-    KH_CASE(KH_EPI_RESID)
-    KH_CASE(KH_EPI_SWIGLU)
-    KH_CASE(KH_EPI_GELU)
-    KH_CASE(KH_EPI_BIAS16)
-    KH_CASE(KH_EPI_BIAS_F32)
-#undef KH_CASE
-    default:
-      return hipErrorInvalidValue;
+    case KH_EPI_STORE16: launch_one<ACT, WF, KH_EPI_STORE16>(a, grid_x, tn, st); break;
+    case KH_EPI_F32: launch_one<ACT, WF, KH_EPI_F32>(a, grid_x, tn, st); break;
+    case KH_EPI_RESID_GATE: launch_one<ACT, WF, KH_EPI_RESID_GATE>(a, grid_x, tn, st); break;
+    case KH_EPI_RESID: launch_one<ACT, WF, KH_EPI_RESID>(a, grid_x, tn, st); break;
+    case KH_EPI_SWIGLU: launch_one<ACT, WF, KH_EPI_SWIGLU>(a, grid_x, tn, st); break;
+    case KH_EPI_GELU: launch_one<ACT, WF, KH_EPI_GELU>(a, grid_x, tn, st); break;
+    case KH_EPI_BIAS16: launch_one<ACT, WF, KH_EPI_BIAS16>(a, grid_x, tn, st); break;
+    case KH_EPI_BIAS_F32: launch_one<ACT, WF, KH_EPI_BIAS_F32>(a, grid_x, tn, st); break;
+    default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
@@ -605,13 +616,7 @@ hipError_t launch_wf(int wf, int epi, const GemmArgs& a, int g, int tn, hipStrea
 
 template <int ACT>
 hipError_t launch_conv(const GemmArgs& a, int grid_x, int tn, hipStream_t st) {
-  dim3 grid(grid_x), block(64 * WAVES_DEFAULT);
-  if (a.sk_iters > 0)
-    hipLaunchKernelGGL((gemm_kernel<ACT, WF_16, KH_EPI_BIAS16, WAVES_DEFAULT, true, BN, true>), grid, block, 0, st, a);
-  else if (tn == 192)
-    hipLaunchKernelGGL((gemm_kernel<ACT, WF_16, KH_EPI_BIAS16, WAVES_DEFAULT, false, 192, true>), grid, block, 0, st, a);
-  else
-    hipLaunchKernelGGL((gemm_kernel<ACT, WF_16, KH_EPI_BIAS16, WAVES_DEFAULT, false, BN, true>), grid, block, 0, st, a);
+  launch_one<ACT, WF_16, KH_EPI_BIAS16, true>(a, grid_x, tn, st);
   return hipGetLastError();
 }
 
@@ -674,26 +679,39 @@ const SkWorkspace* sk_workspace(int dev, hipStream_t st, int ctas) {
 }
 
 // KH_GEMM_TN192=0 keeps every data-parallel launch on 256-wide tiles (read per call)
-bool tn192_enabled() {
+bool narrow_enabled() {
   const char* e = getenv("KH_GEMM_TN192");
   return !(e && e[0] == '0');
 }
 
-// Data-parallel (one tile per workgroup) unless the tiles fill the last wave of workgroups poorly; then
-// stream-K spreads the tiles' K steps evenly over one wave of workgroups.
-void plan_launch(GemmArgs& a, int epi, hipStream_t st, int& grid_x, int& tn) {
+// Tile width and launch. The width is the one that pads N least (ties to the wider: 256, then 192, then
+// 128, which only 16-bit-weight GEMMs have: narrow128). With 256-wide tiles the launch is data-parallel
+// (one tile per workgroup) unless the tiles fill the last wave of workgroups poorly; then stream-K spreads
+// the tiles' K steps evenly over one wave of workgroups. Narrow tiles are data-parallel, unless they fill
+// under 60 % of their last wave and 256-wide stream-K needs less work per CU (padded width x tiles / CUs
+// against waves x width).
+void plan_launch(GemmArgs& a, int epi, hipStream_t st, int& grid_x, int& tn, bool narrow128 = false) {
   const int tiles_m = (a.M + BM - 1) / BM;
-  const int tiles = ((a.N + BN - 1) / BN) * tiles_m;
   const int nk = a.K / BK;
-  grid_x = tiles;
+  auto padded = [&](int w) { return (a.N + w - 1) / w * w; };
+  int dev = 0;
+  const int ctas = hipGetDevice(&dev) == hipSuccess ? sk_cta_count(dev) : 0;
   tn = BN;
+  if (epi != KH_EPI_SWIGLU && narrow_enabled()) {
+    if (padded(192) < padded(tn)) tn = 192;
+    if (narrow128 && padded(128) < padded(tn)) tn = 128;
+    if (tn != BN && ctas > 0 && sk_enabled()) {
+      const int t = (a.N + tn - 1) / tn * tiles_m, r = (t + ctas - 1) / ctas;
+      const double sk_cost = (double)padded(BN) / BN * tiles_m * BN / ctas;
+      if ((double)t / ((double)r * ctas) < 0.6 && sk_cost < (double)r * tn) tn = BN;
+    }
+  }
+  const int tiles = ((a.N + tn - 1) / tn) * tiles_m;
+  grid_x = tiles;
   a.sk_iters = 0;
   a.ws = nullptr;
   a.cnt = nullptr;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return;
-  const int ctas = sk_cta_count(dev);
-  if (ctas <= 0) return;
+  if (tn != BN || ctas <= 0) return;
   const int rounds = (tiles + ctas - 1) / ctas;
   // Stream-K staggers the workgroups' K offsets, so neighbouring tiles no longer share X / W panels in L2
   // at the same time: measured, it loses to data-parallel launches that fill >= 75 % of their last wave
@@ -714,7 +732,7 @@ void plan_launch(GemmArgs& a, int epi, hipStream_t st, int& grid_x, int& tn) {
   // 192-wide tiles where 256-wide ones leave part of a single wave of workgroups idle and 192-wide ones still
   // fit in one wave (4096 x 3072 outputs: 256 tiles instead of 192; measured 349 -> 326 us at K = 12288).
   // Not where they add a partial wave: at 4608 x 12288 (864 vs 1152 tiles) they measured 390 -> 410 us.
-  if (epi != KH_EPI_SWIGLU && a.N % 192 == 0 && tn192_enabled() && tiles < ctas) {
+  if (epi != KH_EPI_SWIGLU && a.N % 192 == 0 && narrow_enabled() && tiles < ctas) {
     const int tiles192 = (a.N / 192) * tiles_m;
     if (tiles192 > tiles && tiles192 <= ctas) {
       tn = 192;
@@ -767,7 +785,7 @@ int gemm(hipStream_t st, int epi, const void* A, int a_dtype, const kh_weight& W
   while ((BK << gshift) < group) gshift++;
   GemmArgs a{A, W.w, W.s, C, (const float*)vec, M, N, K, lda, ldw, ldc, gshift, W.s_dtype, 0, nullptr, nullptr};
   int grid_x = 0, tn = BN;
-  plan_launch(a, epi, st, grid_x, tn);
+  plan_launch(a, epi, st, grid_x, tn, wf == WF_16);
   hipError_t r = a_dtype == KH_F16 ? launch_wf<KH_F16>(wf, epi, a, grid_x, tn, st)
                                    : launch_wf<KH_BF16>(wf, epi, a, grid_x, tn, st);
   if (r != hipSuccess) return e.hip(r, "gemm launch");
@@ -795,7 +813,7 @@ int conv3x3(hipStream_t st, const void* x, int ldx, int C, int H, int W, int up,
   GemmArgs a{x, Wt.w, nullptr, y, bias, H * W, N, K, ldx, N, ldy, 0, KH_F32, 0, nullptr, nullptr,
              C, H, W, up ? 1 : 0, (uint32_t)((((uint64_t)1 << 32) + (uint64_t)C - 1) / (uint64_t)C)};
   int grid_x = 0, tn = BN;
-  plan_launch(a, KH_EPI_BIAS16, st, grid_x, tn);
+  plan_launch(a, KH_EPI_BIAS16, st, grid_x, tn, true);
   const hipError_t r = dtype == KH_F16 ? launch_conv<KH_F16>(a, grid_x, tn, st) : launch_conv<KH_BF16>(a, grid_x, tn, st);
   if (r != hipSuccess) return e.hip(r, "conv3x3 launch");
   return KH_OK;
