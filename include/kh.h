@@ -219,14 +219,15 @@ int kh_download(kh_stream s, void* dst, const void* src, size_t bytes, char* err
 /* ---- VAE decoder (Qwen-Image / Wan 2.1 VAE, single frame), NHWC bf16 activations [pixel, channel] ----
  * The convolutions run on the GEMM core against the converter's Wt[(ky*3+kx)*Cin + ci, co] 16-bit weights
  * (tools/convert.py:338-344); the other calls are the steps around them. */
-/* y[p, n] = bias[n] + sum_k x~[p, k] Wt[k, n]: 3x3 convolution, zero padding 1, as an implicit GEMM (the
+/* y[p, n] = bias[n] + sum_k x~[p, k] Wt[k, n] (+ res[p, n]): 3x3 convolution, zero padding 1, as an implicit GEMM (the
  * activation tiles are gathered from x per (tap, channel), no im2col panel). x: NHWC [pixels, ldx] with C
  * channels, H x W output pixels (up = 1: x is H/2 x W/2, nearest-upsampled first). Wt [K, N] 16-bit of the
  * activation type (dtype KH_F16 / KH_BF16), rows >= 9 C (up to K, a multiple of 64) are multiplied by zero
- * activations; bias f32 [N]; y [H W, ldy]. C, ldx, ldy multiples of 8, N of 64; 16-byte aligned.
+ * activations; bias f32 [N]; res (NULL or 16-bit [H W, ldy], the residual, added after the biased output is
+ * rounded to 16 bits, then rounded again); y [H W, ldy]. C, ldx, ldy multiples of 8, N of 64; 16-byte aligned.
  * Replaces VAEDecoder::conv mode 3 (engine/src/vae.mm:112-125, kernels/vae.metal vconv3x3). */
 int kh_vae_conv3x3(kh_stream stream, const void* x, int ldx, int C, int H, int W, int up, int dtype, const kh_weight* Wt,
-                   int K, int N, const float* bias, void* y, int ldy, char* err, int errlen);
+                   int K, int N, const float* bias, const void* res, void* y, int ldy, char* err, int errlen);
 /* 3x3 (zero padding 1) im2col of output pixels [m0, m0 + rows) of an H x W output: col[r, tap * C + ci],
  * columns [9 C, Kpad) zero; up = 1: x is H/2 x W/2 and nearest-upsampled (the vconv A loader,
  * engine/kernels/vae.metal:11-28). C, ldx, Kpad multiples of 8. */

@@ -82,11 +82,11 @@ int kh_dit_forward(kh_stream stream, const kh_dit_config* cfg, const kh_dit_laye
 
 /* ---- VAE decoder ---- */
 int kh_vae_conv3x3(kh_stream stream, const void* x, int ldx, int C, int H, int W, int up, int dtype, const kh_weight* Wt,
-                   int K, int N, const float* bias, void* y, int ldy, char* err, int errlen) {
+                   int K, int N, const float* bias, const void* res, void* y, int ldy, char* err, int errlen) {
   kh::Err e{err, errlen};
   e.clear();
   if (!Wt) return e.fail("conv3x3: null weight descriptor");
-  return kh::conv3x3((hipStream_t)stream, x, ldx, C, H, W, up, dtype, *Wt, K, N, bias, y, ldy, e);
+  return kh::conv3x3((hipStream_t)stream, x, ldx, C, H, W, up, dtype, *Wt, K, N, bias, res, y, ldy, e);
 }
 
 int kh_vae_im2col(kh_stream stream, const void* x, int ldx, int C, int H, int W, int up, int m0, int rows, void* col,

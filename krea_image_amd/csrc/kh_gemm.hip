@@ -70,6 +70,10 @@ struct GemmArgs {
   // cv_up: the image is cv_H / 2 x cv_W / 2, nearest-upsampled. cv_cinv = ceil(2^32 / cv_C).
   int cv_C, cv_H, cv_W, cv_up;
   uint32_t cv_cinv;
+  // BIAS16 only: C16 = round16(round16(acc + vec) + R) with R 16-bit [M, ldr] (the VAE's residual adds),
+  // when R is not null
+  const void* R;
+  int ldr;
 };
 
 // 16 zero bytes in device memory (never written): the source of the activation DMA for the taps of a
@@ -555,6 +559,14 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
         f32x4 x = *(const f32x4*)gp;
         x += __builtin_bit_cast(f32x4, v);
         *(f32x4*)gp = x;
+      } else if (EPI == KH_EPI_BIAS16 && p.R) {
+        const u32x4 r = *(const u32x4*)((const uint16_t*)p.R + (size_t)gm_ * p.ldr + gcol);
+        u32x4 o;
+#pragma unroll
+        for (int h = 0; h < 4; h++)
+          o[h] = pack16<ACT>(from16<ACT>((uint16_t)v[h]) + from16<ACT>((uint16_t)r[h]),
+                             from16<ACT>((uint16_t)(v[h] >> 16)) + from16<ACT>((uint16_t)(r[h] >> 16)));
+        *(u32x4*)gp = o;
       } else {
         *(u32x4*)gp = v;
       }
@@ -797,7 +809,7 @@ int gemm(hipStream_t st, int epi, const void* A, int a_dtype, const kh_weight& W
 namespace kh {
 
 int conv3x3(hipStream_t st, const void* x, int ldx, int C, int H, int W, int up, int dtype, const kh_weight& Wt, int K,
-            int N, const float* bias, void* y, int ldy, Err& e) {
+            int N, const float* bias, const void* res, void* y, int ldy, Err& e) {
   if (dtype != KH_F16 && dtype != KH_BF16) return e.fail("conv3x3: dtype must be f16 or bf16");
   if (!x || !Wt.w || !y || !bias) return e.fail("conv3x3: null x / W / bias / y");
   if (Wt.w_dtype != dtype) return e.fail("conv3x3: weights must be 16-bit of the activation type");
@@ -809,9 +821,10 @@ int conv3x3(hipStream_t st, const void* x, int ldx, int C, int H, int W, int up,
   if (N % 64) return e.fail("conv3x3: N=%d must be a multiple of 64", N);
   if (ldy < N || ldy % 8) return e.fail("conv3x3: ldy=%d must be >= N and a multiple of 8", ldy);
   if ((long long)H * W >= (1LL << 31)) return e.fail("conv3x3: too many pixels");
-  if (((uintptr_t)x | (uintptr_t)Wt.w | (uintptr_t)y) & 15) return e.fail("conv3x3: x, W and y must be 16-byte aligned");
+  if (((uintptr_t)x | (uintptr_t)Wt.w | (uintptr_t)y | (uintptr_t)res) & 15)
+    return e.fail("conv3x3: x, W, res and y must be 16-byte aligned");
   GemmArgs a{x, Wt.w, nullptr, y, bias, H * W, N, K, ldx, N, ldy, 0, KH_F32, 0, nullptr, nullptr,
-             C, H, W, up ? 1 : 0, (uint32_t)((((uint64_t)1 << 32) + (uint64_t)C - 1) / (uint64_t)C)};
+             C, H, W, up ? 1 : 0, (uint32_t)((((uint64_t)1 << 32) + (uint64_t)C - 1) / (uint64_t)C), res, ldy};
   int grid_x = 0, tn = BN;
   plan_launch(a, KH_EPI_BIAS16, st, grid_x, tn, true);
   const hipError_t r = dtype == KH_F16 ? launch_conv<KH_F16>(a, grid_x, tn, st) : launch_conv<KH_BF16>(a, grid_x, tn, st);

@@ -35,7 +35,7 @@ struct Err {
 int gemm(hipStream_t st, int epi, const void* A, int a_dtype, const kh_weight& W, void* C, int M, int N, int K,
          int lda, int ldw, int ldc, const void* vec, Err& e);
 int conv3x3(hipStream_t st, const void* x, int ldx, int C, int H, int W, int up, int dtype, const kh_weight& Wt, int K,
-            int N, const float* bias, void* y, int ldy, Err& e);
+            int N, const float* bias, const void* res, void* y, int ldy, Err& e);
 
 int attention(hipStream_t st, const void* Q, const void* K, const void* V, void* O, int dtype, int Lq, int Lk,
               int heads, int ldq, int ldk, int ldv, int ldo, int group, int causal, int q_pos0, const void* G,

@@ -129,13 +129,9 @@ class Decoder {
     const int H = up ? 2 * x.H : x.H, Wd = up ? 2 * x.W : x.W;
     if ((rc = acquire(H, Wd, cout, Np, y))) return rc;
     const kh_weight wt{W, nullptr, KH_BF16, KH_F32, 0};
-    if ((rc = kh::conv3x3(st_, x.p, x.ld, x.C, H, Wd, up, KH_BF16, wt, Kp, Np, bias, y.p, Np, e_))) return rc;
-    const long long P = (long long)H * Wd;
-    if (res) {
-      if (res->ld != y.ld || res->P() != P) return e_.fail("vae: residual shape mismatch");
-      if ((rc = vae_add(st_, y.p, res->p, P * y.ld, e_))) return rc;
-    }
-    return KH_OK;
+    if (res && (res->ld != y.ld || res->P() != y.P())) return e_.fail("vae: residual shape mismatch");
+    // the residual add is fused into the GEMM epilogue (the reference's vconv res input, vae.mm:112-125)
+    return kh::conv3x3(st_, x.p, x.ld, x.C, H, Wd, up, KH_BF16, wt, Kp, Np, bias, res ? res->p : nullptr, y.p, Np, e_);
   }
 
   // 1 x 1 conv x.C -> cout (+ residual): a plain GEMM on the activation rows

@@ -178,32 +178,60 @@ __global__ __launch_bounds__(256) void vae_softmax_kernel(const float* __restric
 }
 
 // ---- final 3 x 3 conv C -> 4 (RGBA; alpha's weights are zero and its bias 1) + clamp(-1, 1) + [0, 255]
-//      quantization; one thread per pixel ----
+//      quantization. A workgroup owns a 16 x 16 pixel tile, one pixel per thread. Per chunk of 32
+//      channels it stages the 18 x 18 halo (zero outside the image) and the chunk's weights (f32
+//      [tap][channel][4]) in LDS with coalesced loads, then every thread reads its 9 taps from LDS. The halo's
+//      pixel stride is 40 channels (80 B): the 16 lanes of one 16-byte LDS read cycle then start on 16
+//      distinct 4-bank groups. ----
+constexpr int CO_T = 16, CO_HALO = CO_T + 2, CO_CC = 32, CO_PS = 40;
 __global__ __launch_bounds__(256) void vae_conv_out_kernel(const uint16_t* __restrict__ x, int ldx, int C,
                                                           const uint16_t* __restrict__ w, const float* __restrict__ bias,
                                                           uint8_t* __restrict__ rgba, int H, int W) {
-  const int pix = blockIdx.x * 256 + threadIdx.x;
-  if (pix >= H * W) return;
-  const int y = pix / W, xx = pix % W;
+  __shared__ __attribute__((aligned(16))) uint16_t tile[CO_HALO * CO_HALO * CO_PS];
+  __shared__ f32x4 ws[9 * CO_CC];
+  const int tiles_x = (W + CO_T - 1) / CO_T;
+  const int y0 = (blockIdx.x / tiles_x) * CO_T, x0 = (blockIdx.x % tiles_x) * CO_T;
+  const int ty = threadIdx.x / CO_T, tx = threadIdx.x % CO_T;
+  const int y = y0 + ty, xx = x0 + tx;
   float acc[4] = {bias[0], bias[1], bias[2], bias[3]};
-  for (int tap = 0; tap < 9; tap++) {
-    const int sy = y + tap / 3 - 1, sx = xx + tap % 3 - 1;
-    if (sy < 0 || sy >= H || sx < 0 || sx >= W) continue;
-    const uint16_t* ip = x + ((size_t)sy * W + sx) * ldx;
-    const uint16_t* wp = w + (size_t)tap * C * 4;
-    for (int c = 0; c < C; c += 8) {
-      const u32x4v v = *(const u32x4v*)(ip + c);
+  for (int c0 = 0; c0 < C; c0 += CO_CC) {
+    const int cn = min(CO_CC, C - c0);  // a multiple of 8
+    __syncthreads();  // the previous chunk is no longer read
+    // halo: CO_HALO^2 pixels x cn / 8 chunks of 16 bytes
+    const int gpp = cn / 8;
+    for (int i = threadIdx.x; i < CO_HALO * CO_HALO * gpp; i += 256) {
+      const int hp = i / gpp, g = i - hp * gpp;
+      const int sy = y0 - 1 + hp / CO_HALO, sx = x0 - 1 + hp % CO_HALO;
+      u32x4v v = {0u, 0u, 0u, 0u};
+      if (sy >= 0 && sy < H && sx >= 0 && sx < W) v = *(const u32x4v*)(x + ((size_t)sy * W + sx) * ldx + c0 + 8 * g);
+      *(u32x4v*)(tile + hp * CO_PS + 8 * g) = v;
+    }
+    for (int i = threadIdx.x; i < 9 * cn; i += 256) {
+      const int tap = i / cn, c = i - tap * cn;
+      const uint2 wv = *(const uint2*)(w + ((size_t)tap * C + c0 + c) * 4);
+      ws[tap * CO_CC + c] = (f32x4){bf((uint16_t)wv.x), bf((uint16_t)(wv.x >> 16)), bf((uint16_t)wv.y),
+                                    bf((uint16_t)(wv.y >> 16))};
+    }
+    __syncthreads();
 #pragma unroll
-      for (int k = 0; k < 8; k++) {
-        const float a = bf((uint16_t)(v[k >> 1] >> (16 * (k & 1))));
-        const uint2 wv = *(const uint2*)(wp + (size_t)(c + k) * 4);
-        acc[0] += a * bf((uint16_t)wv.x);
-        acc[1] += a * bf((uint16_t)(wv.x >> 16));
-        acc[2] += a * bf((uint16_t)wv.y);
-        acc[3] += a * bf((uint16_t)(wv.y >> 16));
+    for (int tap = 0; tap < 9; tap++) {
+      const uint16_t* ip = tile + ((ty + tap / 3) * CO_HALO + tx + tap % 3) * CO_PS;
+      const f32x4* wp = ws + tap * CO_CC;
+      for (int c = 0; c < cn; c += 8) {
+        const u32x4v v = *(const u32x4v*)(ip + c);
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+          const float a = bf((uint16_t)(v[k >> 1] >> (16 * (k & 1))));
+          const f32x4 wk = wp[c + k];
+          acc[0] += a * wk[0];
+          acc[1] += a * wk[1];
+          acc[2] += a * wk[2];
+          acc[3] += a * wk[3];
+        }
       }
     }
   }
+  if (y >= H || xx >= W) return;
   uint32_t out = 0;
 #pragma unroll
   for (int k = 0; k < 4; k++) {
@@ -211,7 +239,7 @@ __global__ __launch_bounds__(256) void vae_conv_out_kernel(const uint16_t* __res
     const float u = rintf(fminf(fmaxf(a * 0.5f + 0.5f, 0.f), 1.f) * 255.f);
     out |= (uint32_t)u << (8 * k);
   }
-  ((uint32_t*)rgba)[pix] = out;
+  ((uint32_t*)rgba)[(size_t)y * W + xx] = out;
 }
 
 // ---- zero-padded copy of a weight Wt[K, N] (row stride N) into [Kp, Np], and of a bias [N] into [Np] ----
@@ -305,7 +333,9 @@ int vae_conv_out(hipStream_t st, const void* x, int ldx, int C, const void* w, c
   if (!x || !w || !bias || !rgba) return e.fail("vae_conv_out: null pointer");
   if (C <= 0 || C % 8 || ldx < C || ldx % 8 || H <= 0 || W <= 0) return e.fail("vae_conv_out: bad shape");
   if (((uintptr_t)x & 15) || ((uintptr_t)w & 7) || ((uintptr_t)rgba & 3)) return e.fail("vae_conv_out: alignment");
-  hipLaunchKernelGGL(vae_conv_out_kernel, dim3(blocks((long long)H * W, 256)), dim3(256), 0, st, (const uint16_t*)x,
+  const long long tiles = (long long)((H + CO_T - 1) / CO_T) * ((W + CO_T - 1) / CO_T);
+  if (tiles >= (1LL << 31)) return e.fail("vae_conv_out: image too large");
+  hipLaunchKernelGGL(vae_conv_out_kernel, dim3((unsigned)tiles), dim3(256), 0, st, (const uint16_t*)x,
                      ldx, C, (const uint16_t*)w, bias, (uint8_t*)rgba, H, W);
   const hipError_t r = hipGetLastError();
   return r == hipSuccess ? KH_OK : e.hip(r, "vae_conv_out launch");

@@ -109,7 +109,7 @@ def _bind(lib):
     lib.kh_vae_decode.argtypes = [vp, vp, vp, i, i, vp, sz, vp, cp, i]
     lib.kh_vae_decode.restype = i
     lib.kh_vae_im2col.argtypes = [vp, vp, i, i, i, i, i, i, i, vp, i, cp, i]
-    lib.kh_vae_conv3x3.argtypes = [vp, vp, i, i, i, i, i, i, vp, i, i, vp, vp, i, cp, i]
+    lib.kh_vae_conv3x3.argtypes = [vp, vp, i, i, i, i, i, i, vp, i, i, vp, vp, vp, i, cp, i]
     lib.kh_vae_norm_silu.argtypes = [vp, vp, i, vp, vp, i, i, i, i, cp, i]
     lib.kh_vae_unpack.argtypes = [vp] * 7 + [i, i, cp, i]
     lib.kh_vae_softmax.argtypes = [vp, vp, i, i, i, ctypes.c_float, vp, cp, i]
@@ -129,19 +129,24 @@ def _dp(t):
     return ctypes.c_void_p(t.data_ptr() if hasattr(t, "data_ptr") else int(t))
 
 
-def conv3x3(x, ldx, C, H, W, up, w, K, N, bias, y, ldy):
-    """VAEDecoder::conv mode 3 (engine/src/vae.mm:112-125): implicit-GEMM 3x3 conv, y = conv(x) + bias.
-    w: 16-bit Wt [K, N] (K >= 9 C, a multiple of 64); H x W output pixels (up: x is H/2 x W/2)."""
+def conv3x3(x, ldx, C, H, W, up, w, K, N, bias, y, ldy, res=None):
+    """VAEDecoder::conv mode 3 (engine/src/vae.mm:112-125): implicit-GEMM 3x3 conv, y = conv(x) + bias
+    (+ res, added after the 16-bit rounding of the biased output). w: 16-bit Wt [K, N] (K >= 9 C, a multiple
+    of 64); H x W output pixels (up: x is H/2 x W/2); res like y."""
     P, Pin = H * W, (H // 2) * (W // 2) if up else H * W
     kh._need(x, "x", Pin, C, ldx, x.element_size())
     kh._need(w, "W", K, N, N, 2)
     kh._need(bias, "bias", 1, N, N, 4)
     kh._need(y, "y", P, N, ldy, y.element_size())
+    if res is not None:
+        kh._need(res, "res", P, N, ldy, res.element_size())
+        if res.dtype != x.dtype:
+            raise kh.KhError("conv3x3: res must have the activation type")
     if w.dtype != x.dtype or y.dtype != x.dtype or bias.dtype != torch.float32:
         raise kh.KhError("conv3x3: x, w and y share one 16-bit type; bias is f32")
     wc = kh.Weight(w).c()
     _call(_bind(kh.load()).kh_vae_conv3x3, kh._stream(), _dp(x), ldx, C, H, W, up, kh.dtype_code(x.dtype),
-          ctypes.byref(wc), K, N, _dp(bias), _dp(y), ldy)
+          ctypes.byref(wc), K, N, _dp(bias), None if res is None else _dp(res), _dp(y), ldy)
 
 
 def im2col(x, ldx, C, H, W, up, m0, rows, col, Kpad):

@@ -52,6 +52,13 @@ def test_conv3x3_implicit(dev, H, W, C, N, up):
     torch.cuda.synchronize()
     got = y.view(torch.int16).cpu().numpy().view(np.uint16)
     np.testing.assert_array_equal(got, y2.view(torch.int16).cpu().numpy().view(np.uint16))
+    # fused residual: round16(round16(conv + bias) + res), bit for bit
+    R = _bf(rng.standard_normal((P, N)))
+    y3 = torch.empty(P, N, dtype=torch.bfloat16, device=dev)
+    vae.conv3x3(xd, ldx, C, H, W, up, wd, K, N, bd, y3, N, res=_dev16(R, dev))
+    torch.cuda.synchronize()
+    want = O.from_f32(O.to_f32(got, O.BF16) + O.to_f32(R, O.BF16), O.BF16)
+    np.testing.assert_array_equal(y3.view(torch.int16).cpu().numpy().view(np.uint16), want)
     ref = O.vae_conv(x[:, :C], H, W, w[:9 * C], bias, N, ks=3, up=up)
     g, r = O.to_f32(got, O.BF16), O.to_f32(ref, O.BF16)
     rel = float(np.linalg.norm(g - r) / np.linalg.norm(r))
