@@ -100,6 +100,18 @@ int kh_qk_norm_rope(kh_stream stream, void* qkv, int dtype, const float* wq, con
                     const float* sinb, int rows, int ld, int q_off, int n_q, int k_off, int n_k, float eps,
                     int rope_mode, int big_dim, float* qbig, float* kbig, char* err, int errlen);
 
+/* kh_gemm (epilogue STORE16, C 16-bit [M, ldc]) followed by kh_qk_norm_rope on its output rows, fused: the
+ * norm and RoPE run in the GEMM epilogue on the 16-bit-rounded projection values (the values the separate
+ * pass reads), so the q / k heads never make a round trip through HBM. Arguments as for the two calls, with
+ * the projection output C in place of qkv (rows = M, ld = ldc); q_off and k_off multiples of 128; norm
+ * weights and tables 16-byte aligned. The per-head sum of squares is added in a different order than the
+ * separate pass (results agree to rounding). Replaces the pair Metal::gemm(Epi::BF16) + Metal::qk_norm_rope of
+ * DiT::layer (engine/src/model.mm:373-375). */
+int kh_gemm_qk_norm_rope(kh_stream stream, const void* A, int a_dtype, const kh_weight* W, void* C, int M, int N,
+                         int K, int lda, int ldw, int ldc, const float* wq, const float* wk, const float* cosb,
+                         const float* sinb, int q_off, int n_q, int k_off, int n_k, float eps, int rope_mode,
+                         int big_dim, float* qbig, float* kbig, char* err, int errlen);
+
 /* adaLN modulation GEMV: y[r, n] = (y[r, n] if act & 2) + sum_k act1(x[r, k]) W~[k, n] + bias[n] (bias may be
  * NULL), act & 1 = SiLU on load; rows 1..4, x [rows, K] / y [rows, N] f32, W as in kh_gemm (int8 per-channel or
  * group, or 16-bit). Column sums are combined with f32 atomics (summation order not fixed).

@@ -29,6 +29,17 @@ int kh_rms_norm(kh_stream stream, const float* x, const float* mul, const float*
   return kh::rms_norm((hipStream_t)stream, x, mul, add, y, out_dtype, rows, width, ld_in, ld_out, eps, center, e);
 }
 
+int kh_gemm_qk_norm_rope(kh_stream stream, const void* A, int a_dtype, const kh_weight* W, void* C, int M, int N,
+                         int K, int lda, int ldw, int ldc, const float* wq, const float* wk, const float* cosb,
+                         const float* sinb, int q_off, int n_q, int k_off, int n_k, float eps, int rope_mode,
+                         int big_dim, float* qbig, float* kbig, char* err, int errlen) {
+  kh::Err e{err, errlen};
+  e.clear();
+  if (!W) return e.fail("gemm_qk_norm_rope: null weight descriptor");
+  const kh::QkNormRope q{wq, wk, cosb, sinb, qbig, kbig, q_off, n_q, k_off, n_k, rope_mode, big_dim, eps};
+  return kh::gemm_qk_norm_rope((hipStream_t)stream, A, a_dtype, *W, C, M, N, K, lda, ldw, ldc, q, e);
+}
+
 int kh_qk_norm_rope(kh_stream stream, void* qkv, int dtype, const float* wq, const float* wk, const float* cosb,
                     const float* sinb, int rows, int ld, int q_off, int n_q, int k_off, int n_k, float eps,
                     int rope_mode, int big_dim, float* qbig, float* kbig, char* err, int errlen) {

@@ -49,6 +49,9 @@ int dit_layer_forward(hipStream_t st, const kh_dit_config& c, const kh_dit_layer
   const float* m = s.mods;
   // attention half
   if ((rc = rms_norm(st, s.x, m, m + D, s.h, c.dtype, R, D, D, D, c.eps, c.norm_center, e))) return rc;
+  // QKV projection, then the per-head q / k RMSNorm + RoPE as its own HBM-bound pass (model.mm:373-375). The
+  // fused form (gemm_qk_norm_rope) measured slower at 4608 rows: 304 us against 264 + 25 us, because the GEMM
+  // epilogue runs with the MFMAs idle and its per-row table loads are latency-bound there.
   if ((rc = gemm(st, KH_EPI_STORE16, s.h, c.dtype, L.qkv, s.qkv, R, nqkv, D, D, nqkv, nqkv, nullptr, e))) return rc;
   if ((rc = qk_norm_rope(st, s.qkv, c.dtype, L.qn, L.kn, s.cosb, s.sinb, R, nqkv, 0, c.heads, D, c.kv_heads, c.eps,
                          c.rope_mode, L.big_dim, s.qbig, s.kbig, e)))

@@ -34,6 +34,15 @@ struct Err {
 
 int gemm(hipStream_t st, int epi, const void* A, int a_dtype, const kh_weight& W, void* C, int M, int N, int K,
          int lda, int ldw, int ldc, const void* vec, Err& e);
+// the per-head RMSNorm + RoPE of qk_norm_rope fused into a STORE16 GEMM's epilogue
+struct QkNormRope {
+  const float *wq, *wk, *cosb, *sinb;
+  float *qbig, *kbig;
+  int q_off, n_q, k_off, n_k, mode, big_dim;
+  float eps;
+};
+int gemm_qk_norm_rope(hipStream_t st, const void* A, int a_dtype, const kh_weight& W, void* C, int M, int N, int K,
+                      int lda, int ldw, int ldc, const QkNormRope& q, Err& e);
 int conv3x3(hipStream_t st, const void* x, int ldx, int C, int H, int W, int up, int dtype, const kh_weight& Wt, int K,
             int N, const float* bias, const void* res, void* y, int ldy, Err& e);
 

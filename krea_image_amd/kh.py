@@ -32,7 +32,7 @@ SYMBOLS = ["kh_version", "kh_gemm", "kh_attention", "kh_rms_norm", "kh_qk_norm_r
            "kh_qw_open", "kh_qw_close", "kh_qw_count", "kh_qw_version", "kh_qw_meta", "kh_qw_at", "kh_qw_find",
            "kh_qw_upload", "kh_stream_create", "kh_stream_destroy", "kh_stream_sync", "kh_alloc", "kh_free",
            "kh_upload", "kh_download", "kh_vae_conv3x3", "kh_vae_im2col", "kh_vae_norm_silu", "kh_vae_unpack", "kh_vae_softmax",
-           "kh_vae_conv_out", "kh_vae_workspace_bytes", "kh_vae_decode"]
+           "kh_vae_conv_out", "kh_vae_workspace_bytes", "kh_vae_decode", "kh_gemm_qk_norm_rope"]
 
 
 class KhError(RuntimeError):
@@ -90,6 +90,9 @@ def load():
         lib.kh_gemv.argtypes = [vp, vp, ctypes.POINTER(_WeightC), vp, i, i, i, i, i, vp, cp, i]
         lib.kh_make_cond.argtypes = [vp, vp, vp, vp, vp, i, vp, cp, i]
         lib.kh_gemm_f32.argtypes = [vp, vp, vp, vp, i, i, i, i, i, i, i, vp, cp, i]
+        lib.kh_gemm_qk_norm_rope.argtypes = ([vp, vp, i, ctypes.POINTER(_WeightC), vp] + [i] * 6 + [vp] * 4 +
+                                             [i] * 4 + [ctypes.c_float, i, i, vp, vp, cp, i])
+        lib.kh_gemm_qk_norm_rope.restype = i
         lib.kh_rope_tables.argtypes = [i, i, i, i, vp, vp]
         lib.kh_dit_layer_forward.argtypes = [vp, ctypes.POINTER(DitConfig), ctypes.POINTER(DitLayerC),
                                              ctypes.POINTER(DitStateC), i, cp, i]
@@ -233,6 +236,23 @@ def qk_norm_rope(qkv: torch.Tensor, wq, wk, cos, sin, rows: int, ld: int, q_off:
     _call(load().kh_qk_norm_rope, _stream(), _ptr(qkv), dtype_code(qkv.dtype), _ptr(wq), _ptr(wk), _ptr(cos),
           _ptr(sin), rows, ld, q_off, n_q, k_off, n_k, eps, rope_mode, big_dim, _ptr(qbig), _ptr(kbig))
     return qkv
+
+
+def gemm_qk_norm_rope(A: torch.Tensor, W: Weight, C: torch.Tensor, M: int, N: int, K: int, lda: int, ldw: int,
+                      ldc: int, wq, wk, cos, sin, q_off: int, n_q: int, k_off: int, n_k: int, eps: float,
+                      rope_mode: int, big_dim: int = -1, qbig=None, kbig=None):
+    """The QKV projection of DiT::layer (engine/src/model.mm:373-375) as one launch: kh_gemm STORE16 with
+    kh_qk_norm_rope fused into its epilogue (C plays qkv)."""
+    if C.dtype != A.dtype:
+        raise KhError(f"gemm_qk_norm_rope: C must be {A.dtype}")
+    _need(A, "A", M, K, lda, A.element_size())
+    _need(C, "C", M, N, ldc, C.element_size())
+    _need(W.w, "W", K, N, ldw, 1 if W.w.dtype == torch.int8 else 2)
+    wc = W.c()
+    _call(load().kh_gemm_qk_norm_rope, _stream(), _ptr(A), dtype_code(A.dtype), ctypes.byref(wc), _ptr(C), M, N, K,
+          lda, ldw, ldc, _ptr(wq), _ptr(wk), _ptr(cos), _ptr(sin), q_off, n_q, k_off, n_k, eps, rope_mode, big_dim,
+          _ptr(qbig), _ptr(kbig))
+    return C
 
 
 def gemv(x: torch.Tensor, W: Weight, y: torch.Tensor, rows: int, N: int, K: int, ldw: int, act: int = 0, bias=None):

@@ -47,8 +47,9 @@ def test_checker_flags_known_violations():
 
 
 @pytest.mark.skipif(not os.path.exists("/opt/rocm/bin/hipcc"), reason="hipcc not available")
-def test_gemm_kernels_have_no_untracked_load_hazards(tmp_path):
-    text = compile_to_asm(os.path.join(CSRC, "kh_gemm.hip"), str(tmp_path / "gemm.s"), CSRC)
+@pytest.mark.parametrize("unit", ["kh_gemm_f16.hip", "kh_gemm_bf16.hip"])
+def test_gemm_kernels_have_no_untracked_load_hazards(tmp_path, unit):
+    text = compile_to_asm(os.path.join(CSRC, unit), str(tmp_path / "gemm.s"), CSRC)
     res = check_text(text)
     assert len(res) >= 80, f"expected every GEMM instantiation, found {len(res)}"
     bad = {k: v[:3] for k, v in res.items() if v}
