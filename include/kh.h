@@ -80,6 +80,8 @@ int kh_gemm(kh_stream stream, int epi, const void* A, int a_dtype, const kh_weig
  * before P V. Q [Lq, ldq], K [Lk, ldk], V [Lk, ldv], O [Lq, ldo], G [Lq, ldg] (dtype KH_F16 / KH_BF16), head h at
  * column 128 h (kv head at 128 (h / group)). causal: key k visible to query i iff k <= i + q_pos0. QB [Lq, heads]
  * and KB [Lk, heads / group] (f32, both or neither): the rank-1 score term of a "big" head dimension.
+ * Workgroups of 8 x 32 queries (4 x 32 with the rank-1 term; KH_ATTN_WAVES=4 / 8 overrides); either size
+ * computes the same per-query arithmetic.
  * Replaces krea::Metal::attention (engine/src/metal.h:86-88, engine/src/metal.mm:193-202). */
 int kh_attention(kh_stream stream, const void* Q, const void* K, const void* V, void* O, int dtype, int Lq, int Lk,
                  int heads, int ldq, int ldk, int ldv, int ldo, int group, int causal, int q_pos0, const void* G,

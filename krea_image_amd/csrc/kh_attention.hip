@@ -20,11 +20,12 @@
 //  * K tiles stream global -> LDS directly (16-byte DMA per lane), rows of 256 B with the 16-byte chunk
 //    XOR-swizzled by (row & 15). V tiles are transposed on the way in (4 keys x 8 dims per thread,
 //    v_perm_b32 into 8 dims x 4 keys) into V^T rows of 128 B (key order and swizzle: vt_off).
-//  * 4 waves x 32 queries per workgroup, 64-key blocks; K tiles double-buffered, V^T tiles triple-buffered
-//    (80 KB, two workgroups per CU). Software pipeline: block b issues S(b), then P V of block b - 1, and
+//  * 8 waves x 32 queries per workgroup (one per CU; 4 waves and two per CU with the rank-1 term), 64-key
+//    blocks; K tiles double-buffered, V^T tiles triple-buffered (80 KB). Waves 0..3 transpose V. Software pipeline: block b issues S(b), then P V of block b - 1, and
 //    the softmax of block b runs on the VALU while those MFMAs execute.
 //  * Lazy online softmax (the reference's LAZY_TH idea, attention.metal:33-37): the running max only moves
 //    when a block's max exceeds it by more than 8 (log2 units), so most blocks skip the O rescale.
+#include <cstdlib>
 #include <type_traits>
 
 #include "kh_common.h"
@@ -34,7 +35,7 @@ namespace kh {
 
 namespace {
 
-constexpr int D = 128, BQ = 128, BKEYS = 64, NTHR = 256;
+constexpr int D = 128, BKEYS = 64;
 constexpr int KT_BYTES = BKEYS * D * 2;   // K tile: 64 rows x 256 B
 constexpr int VT_BYTES = D * BKEYS * 2;   // V^T tile: 128 rows x 128 B
 constexpr int K_STAGES = 2, V_STAGES = 3;  // V^T lives one block longer: P V of block b - 1 runs in block b
@@ -105,8 +106,11 @@ __device__ __forceinline__ int vt_off(int d, int kq) {
   return d * 128 + (((2 * (kq >> 2) + (kq & 1)) ^ (((d >> 1) ^ (d >> 4)) & 7)) * 16) + ((kq >> 1) & 1) * 8;
 }
 
-template <int DT, bool GATE, bool BIG, bool CAUSAL>
-__global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
+// NW waves x 32 queries per workgroup: 4 (two workgroups per CU) or 8 (one per CU; each K / V tile staged in
+// LDS then feeds twice the MFMA work)
+template <int DT, bool GATE, bool BIG, bool CAUSAL, int NW>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void attn_kernel(AttnArgs p) {
+  constexpr int BQ = 32 * NW;
   // [K stage 0 | K stage 1 | V^T stage 0 | 1 | 2]
   __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];
   typedef __attribute__((address_space(3))) void lds_void;
@@ -147,19 +151,19 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
   const uint16_t* kbase = (const uint16_t*)p.K + kvh * D;
   auto issue_k = [&](int b, int buf) {
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int row = 4 * (4 * r + wave) + (lane >> 4);
+    for (int r = 0; r < 16 / NW; r++) {
+      const int row = 4 * (NW * r + wave) + (lane >> 4);
       const int key = min(b * BKEYS + row, p.Lk - 1);
       const int c = (lane & 15) ^ (row & 15);
       __builtin_amdgcn_global_load_lds((const void*)(kbase + (size_t)key * p.ldk + c * 8),
-                                       (lds_void*)(lds + buf * KT_BYTES + (4 * r + wave) * 1024), 16, 0, 0);
+                                       (lds_void*)(lds + buf * KT_BYTES + (NW * r + wave) * 1024), 16, 0, 0);
     }
   };
   // ---- V tile: thread -> keys 4 vkq .. 4 vkq + 3, dims 8 vc .. 8 vc + 7. Within a wave the four 16-lane
   //      groups take key quads 4w + {0, 2, 1, 3}, so each half wave writes quads of both 8-byte halves of
   //      a chunk (see vt_off) ----
   const int vlane = tid & 63;
-  const int vkq = 4 * wave + (((vlane >> 4) & 1) << 1 | ((vlane >> 5) & 1)), vc = vlane & 15;
+  const int vkq = 4 * (wave & 3) + (((vlane >> 4) & 1) << 1 | ((vlane >> 5) & 1)), vc = vlane & 15;
   const uint16_t* vbase = (const uint16_t*)p.V + kvh * D + vc * 8;
   u32x4 vr[4];
   auto load_v = [&](int b) {
@@ -216,9 +220,9 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
 
   if (nblk > 0) {
     issue_k(0, 0);
-    load_v(0);
+    if (wave < 4) load_v(0);
     load_kb(0);
-    store_vt(0);
+    if (wave < 4) store_vt(0);
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
     lds_barrier();
   }
@@ -232,7 +236,7 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
     const bool has_next = b + 1 < nblk;
     if (has_next) {
       issue_k(b + 1, (b + 1) & 1);
-      load_v(b + 1);
+      if (wave < 4) load_v(b + 1);
     }
     const char* kt = lds + (b & 1) * KT_BYTES;
 
@@ -293,7 +297,7 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
     }
 
     if (has_next) {
-      store_vt((b + 1) % V_STAGES);  // the stage of block b - 2, whose P V ran in block b - 1
+      if (wave < 4) store_vt((b + 1) % V_STAGES);  // the stage of block b - 2, whose P V ran in block b - 1
       __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));  // vmcnt(0): the next K tile has landed
     }
     lds_barrier();
@@ -331,20 +335,34 @@ __global__ __launch_bounds__(NTHR, 2) void attn_kernel(AttnArgs p) {
     }
 }
 
-template <int DT, bool GATE, bool BIG>
-hipError_t launch3(bool causal, const AttnArgs& a, hipStream_t st) {
-  dim3 grid(((a.Lq + BQ - 1) / BQ) * a.heads), block(NTHR);
+template <int DT, bool GATE, bool BIG, int NW>
+hipError_t launch4(bool causal, const AttnArgs& a, hipStream_t st) {
+  dim3 grid(((a.Lq + 32 * NW - 1) / (32 * NW)) * a.heads), block(64 * NW);
   if (causal)
-    hipLaunchKernelGGL((attn_kernel<DT, GATE, BIG, true>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((attn_kernel<DT, GATE, BIG, true, NW>), grid, block, 0, st, a);
   else
-    hipLaunchKernelGGL((attn_kernel<DT, GATE, BIG, false>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((attn_kernel<DT, GATE, BIG, false, NW>), grid, block, 0, st, a);
   return hipGetLastError();
 }
 
+template <int DT, bool GATE, bool BIG>
+hipError_t launch3(bool causal, int nw, const AttnArgs& a, hipStream_t st) {
+  return nw == 8 ? launch4<DT, GATE, BIG, 8>(causal, a, st) : launch4<DT, GATE, BIG, 4>(causal, a, st);
+}
+
 template <int DT>
-hipError_t launch2(bool gate, bool big, bool causal, const AttnArgs& a, hipStream_t st) {
-  if (gate) return big ? launch3<DT, true, true>(causal, a, st) : launch3<DT, true, false>(causal, a, st);
-  return big ? launch3<DT, false, true>(causal, a, st) : launch3<DT, false, false>(causal, a, st);
+hipError_t launch2(bool gate, bool big, bool causal, int nw, const AttnArgs& a, hipStream_t st) {
+  if (gate) return big ? launch3<DT, true, true>(causal, nw, a, st) : launch3<DT, true, false>(causal, nw, a, st);
+  return big ? launch3<DT, false, true>(causal, nw, a, st) : launch3<DT, false, false>(causal, nw, a, st);
+}
+
+// Waves per workgroup: 8 (measured at 4608 tokens: 24 heads 400 -> 324 us; 48 q / 12 kv heads + gate 645 ->
+// 616 us; 8704 tokens x 24 heads 1240 -> 1142 us), except with the rank-1 term, where 4 measured faster
+// (668 vs 698 us). KH_ATTN_WAVES=4 / 8 overrides (read per call).
+int attn_waves(bool big) {
+  const char* e = getenv("KH_ATTN_WAVES");
+  if (e && (e[0] == '4' || e[0] == '8') && e[1] == 0) return e[0] - '0';
+  return big ? 4 : 8;
 }
 
 }  // namespace
@@ -367,8 +385,9 @@ int attention(hipStream_t st, const void* Q, const void* K, const void* V, void*
   if (Lq > (1 << 24) / 1 || (size_t)Lk * ldk > ((size_t)1 << 31)) return e.fail("attention: too large");
   AttnArgs a{Q, K, V, O, G, QB, KB, Lq, Lk, heads, ldq, ldk, ldv, ldo, group, q_pos0, ldg, heads, kv_heads,
              (float)(1.4426950408889634 / 11.313708498984761)};
-  const hipError_t r = dtype == KH_F16 ? launch2<KH_F16>(G != nullptr, QB != nullptr, causal != 0, a, st)
-                                       : launch2<KH_BF16>(G != nullptr, QB != nullptr, causal != 0, a, st);
+  const int nw = attn_waves(QB != nullptr);
+  const hipError_t r = dtype == KH_F16 ? launch2<KH_F16>(G != nullptr, QB != nullptr, causal != 0, nw, a, st)
+                                       : launch2<KH_BF16>(G != nullptr, QB != nullptr, causal != 0, nw, a, st);
   if (r != hipSuccess) return e.hip(r, "attention launch");
   return KH_OK;
 }
