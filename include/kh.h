@@ -242,6 +242,19 @@ int kh_download(kh_stream s, void* dst, const void* src, size_t bytes, char* err
  * Replaces VAEDecoder::conv mode 3 (engine/src/vae.mm:112-125, kernels/vae.metal vconv3x3). */
 int kh_vae_conv3x3(kh_stream stream, const void* x, int ldx, int C, int H, int W, int up, int dtype, const kh_weight* Wt,
                    int K, int N, const float* bias, const void* res, void* y, int ldy, char* err, int errlen);
+/* Sub-pixel weights of a nearest-2x upsample + 3x3 conv (the reference's vae_subpix_weights,
+ * engine/kernels/vae.metal:134-160, driven by engine/src/vae.mm:137-150): W [9 Cin, Cout] 16-bit (dtype) ->
+ * W2 [K, 4 Np] with W2[(2r + s) Cin + ci, (2py + px) Np + co] = 16-bit round of the fp32 sum of the 3x3 taps that
+ * fall on low-res offset (r + py - 1, s + px - 1); rows >= 4 Cin and columns >= Cout of each phase zero.
+ * bias [Cout] f32 (or NULL) -> bias4 [4 Np] (or NULL). K >= 4 Cin, Np >= Cout. */
+int kh_vae_subpix_weights(kh_stream stream, const void* W, int dtype, int Cin, int Cout, void* W2, int K, int Np,
+                          const float* bias, float* bias4, char* err, int errlen);
+/* y = conv3x3(nearest2x(x)) + bias as 4 sub-pixel 2x2 convs in one implicit GEMM (4/9 of the direct form's
+ * multiply-adds): x NHWC [H W, ldx] with C channels (the low-res image), W2 / bias4 from
+ * kh_vae_subpix_weights, y [2H x 2W pixels, ldy] with Np channels (Np a multiple of 128 or 192). Replaces
+ * VAEDecoder::conv mode 2 (engine/src/vae.mm:137-150, vconv_up2). */
+int kh_vae_conv_up2(kh_stream stream, const void* x, int ldx, int C, int H, int W, int dtype, const kh_weight* W2, int K,
+                    int Np, const float* bias4, void* y, int ldy, char* err, int errlen);
 /* 3x3 (zero padding 1) im2col of output pixels [m0, m0 + rows) of an H x W output: col[r, tap * C + ci],
  * columns [9 C, Kpad) zero; up = 1: x is H/2 x W/2 and nearest-upsampled (the vconv A loader,
  * engine/kernels/vae.metal:11-28). C, ldx, Kpad multiples of 8. */

@@ -100,6 +100,21 @@ int kh_vae_conv3x3(kh_stream stream, const void* x, int ldx, int C, int H, int W
   return kh::conv3x3((hipStream_t)stream, x, ldx, C, H, W, up, dtype, *Wt, K, N, bias, res, y, ldy, e);
 }
 
+int kh_vae_subpix_weights(kh_stream stream, const void* W, int dtype, int Cin, int Cout, void* W2, int K, int Np,
+                          const float* bias, float* bias4, char* err, int errlen) {
+  kh::Err e{err, errlen};
+  e.clear();
+  return kh::vae_subpix_weights((hipStream_t)stream, W, dtype, Cin, Cout, W2, K, Np, bias, bias4, e);
+}
+
+int kh_vae_conv_up2(kh_stream stream, const void* x, int ldx, int C, int H, int W, int dtype, const kh_weight* W2, int K,
+                    int Np, const float* bias4, void* y, int ldy, char* err, int errlen) {
+  kh::Err e{err, errlen};
+  e.clear();
+  if (!W2) return e.fail("conv_up2: null weight descriptor");
+  return kh::conv_up2_subpix((hipStream_t)stream, x, ldx, C, H, W, dtype, *W2, K, Np, bias4, y, ldy, e);
+}
+
 int kh_vae_im2col(kh_stream stream, const void* x, int ldx, int C, int H, int W, int up, int m0, int rows, void* col,
                   int Kpad, char* err, int errlen) {
   kh::Err e{err, errlen};

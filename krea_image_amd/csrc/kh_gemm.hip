@@ -85,14 +85,17 @@ bool narrow_enabled() {
 // the tiles' K steps evenly over one wave of workgroups. Narrow tiles are data-parallel, unless they fill
 // under 60 % of their last wave and 256-wide stream-K needs less work per CU (padded width x tiles / CUs
 // against waves x width).
-void plan_launch(GemmArgs& a, int epi, hipStream_t st, int& grid_x, int& tn, bool narrow128 = false) {
+// tn_div > 0: the tile width must divide tn_div (sub-pixel convs: a tile may not straddle two phases).
+void plan_launch(GemmArgs& a, int epi, hipStream_t st, int& grid_x, int& tn, bool narrow128 = false, int tn_div = 0) {
   const int tiles_m = (a.M + BM - 1) / BM;
   const int nk = a.K / BK;
   auto padded = [&](int w) { return (a.N + w - 1) / w * w; };
   int dev = 0;
   const int ctas = hipGetDevice(&dev) == hipSuccess ? sk_cta_count(dev) : 0;
   tn = BN;
-  if (!wide_only(epi) && narrow_enabled()) {
+  if (tn_div > 0) {
+    tn = tn_div % BN == 0 ? BN : tn_div % 192 == 0 ? 192 : 128;
+  } else if (!wide_only(epi) && narrow_enabled()) {
     if (padded(192) < padded(tn)) tn = 192;
     if (narrow128 && padded(128) < padded(tn)) tn = 128;
     if (tn != BN && ctas > 0 && sk_enabled()) {
@@ -124,6 +127,7 @@ void plan_launch(GemmArgs& a, int epi, hipStream_t st, int& grid_x, int& tn, boo
       return;
     }
   }
+  if (tn_div > 0) return;
   // 192-wide tiles where 256-wide ones leave part of a single wave of workgroups idle and 192-wide ones still
   // fit in one wave (4096 x 3072 outputs: 256 tiles instead of 192; measured 349 -> 326 us at K = 12288).
   // Not where they add a partial wave: at 4608 x 12288 (864 vs 1152 tiles) they measured 390 -> 410 us.
@@ -250,3 +254,32 @@ int conv3x3(hipStream_t st, const void* x, int ldx, int C, int H, int W, int up,
 
 }  // namespace kh
 
+
+namespace kh {
+
+int conv_up2_subpix(hipStream_t st, const void* x, int ldx, int C, int H, int W, int dtype, const kh_weight& W2, int K,
+                    int Np, const float* bias4, void* y, int ldy, Err& e) {
+  if (dtype != KH_F16 && dtype != KH_BF16) return e.fail("conv_up2: dtype must be f16 or bf16");
+  if (!x || !W2.w || !y || !bias4) return e.fail("conv_up2: null x / W2 / bias / y");
+  if (W2.w_dtype != dtype) return e.fail("conv_up2: weights must be 16-bit of the activation type");
+  if (H <= 0 || W <= 0 || C <= 0 || Np <= 0) return e.fail("conv_up2: empty shape H=%d W=%d C=%d Np=%d", H, W, C, Np);
+  if (C % 8) return e.fail("conv_up2: C=%d must be a multiple of 8", C);
+  if (ldx < C || ldx % 8) return e.fail("conv_up2: ldx=%d must be >= C and a multiple of 8", ldx);
+  if (K % BK || K < 4 * C) return e.fail("conv_up2: K=%d must be a multiple of 64 and >= 4 C = %d", K, 4 * C);
+  if (Np % 128 && Np % 192) return e.fail("conv_up2: Np=%d must be a multiple of 128 or 192", Np);
+  if (ldy < Np || ldy % 8) return e.fail("conv_up2: ldy=%d must be >= Np and a multiple of 8", ldy);
+  if (4LL * H * W >= (1LL << 31) || W >= (1 << 16)) return e.fail("conv_up2: image too large");
+  if (((uintptr_t)x | (uintptr_t)W2.w | (uintptr_t)y) & 15) return e.fail("conv_up2: x, W2 and y must be 16-byte aligned");
+  GemmArgs a{x, W2.w, nullptr, y, bias4, H * W, 4 * Np, K, ldx, 4 * Np, ldy, 0, KH_F32, 0, nullptr, nullptr,
+             C, H, W, 0, (uint32_t)((((uint64_t)1 << 32) + (uint64_t)C - 1) / (uint64_t)C), nullptr, 0};
+  a.cv_sub = 1;
+  a.cv_np = Np;
+  a.cv_winv = (uint32_t)((((uint64_t)1 << 32) + (uint64_t)W - 1) / (uint64_t)W);
+  int grid_x = 0, tn = BN;
+  plan_launch(a, KH_EPI_BIAS16, st, grid_x, tn, true, Np);
+  const hipError_t r = dtype == KH_F16 ? launch_conv_f16(a, grid_x, tn, st) : launch_conv_bf16(a, grid_x, tn, st);
+  if (r != hipSuccess) return e.hip(r, "conv_up2 launch");
+  return KH_OK;
+}
+
+}  // namespace kh

@@ -42,6 +42,12 @@ struct GemmArgs {
   // when R is not null
   const void* R;
   int ldr;
+  // cv_sub = 1: the 2x-upsampling 3 x 3 conv as sub-pixel 2 x 2 convs on the cv_H x cv_W low-res image: rows
+  // are low-res pixels, K runs over (2 x 2 tap, channel), column n = phase cv_np + co with phase = 2 py + px,
+  // and row (i, j) of phase (py, px) is output pixel (2 i + py, 2 j + px) of the 2 cv_H x 2 cv_W image.
+  // cv_winv = ceil(2^32 / cv_W).
+  int cv_sub, cv_np;
+  uint32_t cv_winv;
   // EPI_QKNR: q heads are columns [qk_qoff, + 128 qk_nq), k heads [qk_koff, + 128 qk_nk) (offsets multiples of
   // 128); norm weights qk_wq / qk_wk [128]; RoPE tables [M, 64] (qk_mode 0: adjacent pairs, 1: i with i + 64,
   // 2: none); qk_big >= 0: that head channel goes to qk_qbig [M, nq] / qk_kbig [M, nk] in f32 and is zeroed

@@ -200,6 +200,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
   const int xchunk = ((lane & 7) ^ swz(xrow0)) * 8;
   int xoff[X_LOADS];
   int cy[CONV ? X_LOADS : 1], cx[CONV ? X_LOADS : 1];  // CONV: output pixel (row, column) of each load's row
+  int sub_py = 0, sub_px = 0;                            // CONV sub-pixel: the tile's phase
   const uint16_t* xbase = (const uint16_t*)p.A;
   auto issue_x_to = [&](int t, int stage) {
     char* dst = lds + stage * STAGE + wave * 1024;
@@ -208,12 +209,18 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
       // image and k >= 9 C read the zero chunk
       const uint32_t k = (uint32_t)((kb + t) * BK + xchunk);
       const int tap = (int)__umulhi(k, p.cv_cinv), ci = (int)k - tap * p.cv_C;
-      const int ty = (tap * 11) >> 5, dy = ty - 1, dx = tap - 3 * ty - 1;  // tap / 3 for tap < 12
+      int dy, dx, ntap;
+      if (p.cv_sub) {  // 2 x 2 taps at low-res offsets (r + py - 1, s + px - 1)
+        dy = (tap >> 1) + sub_py - 1, dx = (tap & 1) + sub_px - 1, ntap = 4;
+      } else {
+        const int ty = (tap * 11) >> 5;  // tap / 3 for tap < 12
+        dy = ty - 1, dx = tap - 3 * ty - 1, ntap = 9;
+      }
       const int win = p.cv_up ? p.cv_W >> 1 : p.cv_W;
 #pragma unroll
       for (int r = 0; r < X_LOADS; r++) {
         int sy = cy[r] + dy, sx = cx[r] + dx;
-        const bool in = tap < 9 && sy >= 0 && sy < p.cv_H && sx >= 0 && sx < p.cv_W;
+        const bool in = tap < ntap && sy >= 0 && sy < p.cv_H && sx >= 0 && sx < p.cv_W;
         sy >>= p.cv_up;
         sx >>= p.cv_up;
         const void* src = in ? (const void*)(xbase + ((size_t)sy * win + sx) * p.lda + ci) : (const void*)g_zero_chunk;
@@ -244,6 +251,12 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
         cx[r] = m - cy[r] * p.cv_W;
       } else {
         xoff[r] = m * p.lda + xchunk;
+      }
+    }
+    if constexpr (CONV) {
+      if (p.cv_sub) {
+        const int ph = n0 / p.cv_np;  // a tile lies in one phase (TN divides cv_np)
+        sub_py = ph >> 1, sub_px = ph & 1;
       }
     }
     wcol = min(n0 + wl * 4, p.N - 4);
@@ -623,13 +636,22 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
       const int gm_ = grow0 + r, gcol = out_n0 + c * (16 / ELEM);
       if (gm_ >= p.M || gcol >= out_N) continue;
       const u32x4 v = *(const u32x4*)(lds + r * ROW_BYTES + c * 16);
-      char* gp = (char*)p.C + ((size_t)gm_ * p.ldc + gcol) * ELEM;
+      size_t orow = (size_t)gm_;
+      int ocol = gcol;
+      if constexpr (CONV) {
+        if (p.cv_sub) {  // low-res pixel (i, j) of phase (py, px) -> output pixel (2 i + py, 2 j + px)
+          const int i = (int)__umulhi((uint32_t)gm_, p.cv_winv), j = gm_ - i * p.cv_W;
+          orow = (size_t)(2 * i + sub_py) * (2 * p.cv_W) + 2 * j + sub_px;
+          ocol = gcol - (2 * sub_py + sub_px) * p.cv_np;
+        }
+      }
+      char* gp = (char*)p.C + (orow * p.ldc + ocol) * ELEM;
       if constexpr (EPI == KH_EPI_RESID || EPI == KH_EPI_RESID_GATE) {
         f32x4 x = *(const f32x4*)gp;
         x += __builtin_bit_cast(f32x4, v);
         *(f32x4*)gp = x;
       } else if (EPI == KH_EPI_BIAS16 && p.R) {
-        const u32x4 r = *(const u32x4*)((const uint16_t*)p.R + (size_t)gm_ * p.ldr + gcol);
+        const u32x4 r = *(const u32x4*)((const uint16_t*)p.R + orow * p.ldr + ocol);
         u32x4 o;
 #pragma unroll
         for (int h = 0; h < 4; h++)

@@ -43,6 +43,10 @@ struct QkNormRope {
 };
 int gemm_qk_norm_rope(hipStream_t st, const void* A, int a_dtype, const kh_weight& W, void* C, int M, int N, int K,
                       int lda, int ldw, int ldc, const QkNormRope& q, Err& e);
+int conv_up2_subpix(hipStream_t st, const void* x, int ldx, int C, int H, int W, int dtype, const kh_weight& W2, int K,
+                    int Np, const float* bias4, void* y, int ldy, Err& e);
+int vae_subpix_weights(hipStream_t st, const void* w, int dtype, int Cin, int Cout, void* w2, int Kp, int Np,
+                       const float* b, float* b4, Err& e);
 int conv3x3(hipStream_t st, const void* x, int ldx, int C, int H, int W, int up, int dtype, const kh_weight& Wt, int K,
             int N, const float* bias, const void* res, void* y, int ldy, Err& e);
 

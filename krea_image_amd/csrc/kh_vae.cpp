@@ -35,8 +35,9 @@ Plan plan(int H16, int W16) {
   // largest activation: P x padded channels over the stages (P0 x 384, 4 P0 x 384, 16 P0 x 192, 64 P0 x 128)
   const long long a = std::max({p.P0 * MID_C, 4 * p.P0 * 384, 16 * p.P0 * ld_of(192), p.P3 * ld_of(96)});
   p.act = (size_t)ru(a * 2, 256);
-  p.wpad = (size_t)ru(9LL * 384 * 384 * 2, 256);
-  p.bpad = (size_t)ru(1152 * 4, 256);
+  // padded 3 x 3 weights [9 C -> 64, C -> 64] or sub-pixel weights [4 C -> 64, 4 Np] (C <= 384) and biases
+  p.wpad = (size_t)ru(16LL * 384 * 384 * 2, 256);
+  p.bpad = (size_t)ru(4 * 1152 * 4, 256);
   p.qkv = (size_t)ru(p.Pp0 * 3 * MID_C * 2, 256);
   p.kt = (size_t)ru((long long)MID_C * p.Pp0 * 2, 256);
   const long long qc = std::min<long long>(QC, p.P0);
@@ -118,6 +119,20 @@ class Decoder {
       return rc;
     const void* W = w;
     const float* bias = (const float*)b;
+    if (up && (Np % 128 == 0 || Np % 192 == 0)) {
+      // nearest-2x + 3 x 3 as four 2 x 2 sub-pixel convs (the reference's mode 2, vae.mm:137-150): folded
+      // weights W2 [4 Cin (-> 64), 4 Np] and a bias per phase in the workspace, then one implicit GEMM
+      const int K2 = (int)ru(4 * x.C, 64);
+      uint16_t* wp = (uint16_t*)(ws_ + pl_.off_wpad);
+      float* bp = (float*)(ws_ + pl_.off_bpad);
+      if ((size_t)K2 * 4 * Np * 2 > pl_.wpad || (size_t)4 * Np * 4 > pl_.bpad)
+        return e_.fail("vae: sub-pixel weight too large");
+      if ((rc = vae_subpix_weights(st_, w, KH_BF16, x.C, cout, wp, K2, Np, bias, bp, e_))) return rc;
+      if (res) return e_.fail("vae: no residual on an upsampling conv");
+      if ((rc = acquire(2 * x.H, 2 * x.W, cout, Np, y))) return rc;
+      const kh_weight w2{wp, nullptr, KH_BF16, KH_F32, 0};
+      return conv_up2_subpix(st_, x.p, x.ld, x.C, x.H, x.W, KH_BF16, w2, K2, Np, bp, y.p, Np, e_);
+    }
     if (Kp != K || Np != cout) {  // the GEMM's K and N multiples of 64: zero rows / columns
       uint16_t* wp = (uint16_t*)(ws_ + pl_.off_wpad);
       float* bp = (float*)(ws_ + pl_.off_bpad);

@@ -253,6 +253,31 @@ __global__ __launch_bounds__(256) void vae_pad_weight_kernel(const uint16_t* __r
   out[i] = (k < K && n < N) ? w[(size_t)k * N + n] : (uint16_t)0;
 }
 
+// ---- sub-pixel weights of a nearest-2x + 3 x 3 conv (engine/kernels/vae.metal:134-160 semantics): for
+//      phase (py, px) = (ph >> 1, ph & 1) and 2 x 2 tap t = (r, s), W2[t Cin + ci, ph Np + co] is the sum of the
+//      3 x 3 taps (ky, kx) that land on low-res offset (r + py - 1, s + px - 1): rows ky in [0, py] for r = 0,
+//      [1 + py, 2] for r = 1 (columns likewise), summed in fp32 in (ky, kx) order, rounded once to 16 bits.
+//      Rows >= 4 Cin and columns co >= Cout of each phase are zero; bias4[ph Np + co] = bias[co] (or 0). ----
+template <int DT>
+__global__ __launch_bounds__(256) void vae_subpix_weights_kernel(const uint16_t* __restrict__ w, int Cin, int Cout,
+                                                                 uint16_t* __restrict__ w2, int Kp, int Np,
+                                                                 const float* __restrict__ b, float* __restrict__ b4) {
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  const int N4 = 4 * Np;
+  if (i < N4 && b4) b4[i] = (b && (int)(i % Np) < Cout) ? b[i % Np] : 0.f;
+  if (i >= (long long)Kp * N4) return;
+  const int row = (int)(i / N4), col = (int)(i % N4);
+  const int ph = col / Np, co = col - ph * Np;
+  float acc = 0.f;
+  if (row < 4 * Cin && co < Cout) {
+    const int t = row / Cin, ci = row - t * Cin, r = t >> 1, sc = t & 1, py = ph >> 1, px = ph & 1;
+    const int y0 = r ? 1 + py : 0, y1 = r ? 2 : py, x0 = sc ? 1 + px : 0, x1 = sc ? 2 : px;
+    for (int ky = y0; ky <= y1; ky++)
+      for (int kx = x0; kx <= x1; kx++) acc += from16<DT>(w[((size_t)(ky * 3 + kx) * Cin + ci) * Cout + co]);
+  }
+  w2[i] = to16<DT>(acc);
+}
+
 // ---- zero n16 16-byte chunks (a kernel, not a memset node, so that a captured decode replays correctly) ----
 __global__ __launch_bounds__(256) void vae_zero_kernel(u32x4v* __restrict__ p, long long n16) {
   for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n16; i += (long long)gridDim.x * 256)
@@ -349,6 +374,22 @@ int vae_zero(hipStream_t st, void* p, size_t bytes, Err& e) {
                      (u32x4v*)p, n16);
   const hipError_t r = hipGetLastError();
   return r == hipSuccess ? KH_OK : e.hip(r, "vae_zero launch");
+}
+
+int vae_subpix_weights(hipStream_t st, const void* w, int dtype, int Cin, int Cout, void* w2, int Kp, int Np,
+                       const float* b, float* b4, Err& e) {
+  if (!w || !w2) return e.fail("vae_subpix_weights: null pointer");
+  if (dtype != KH_F16 && dtype != KH_BF16) return e.fail("vae_subpix_weights: dtype must be f16 or bf16");
+  if (Cin <= 0 || Cout <= 0 || Kp < 4 * Cin || Np < Cout) return e.fail("vae_subpix_weights: bad shape");
+  const long long n = (long long)Kp * 4 * Np;
+  if (dtype == KH_BF16)
+    hipLaunchKernelGGL(vae_subpix_weights_kernel<KH_BF16>, dim3(blocks(n, 256)), dim3(256), 0, st, (const uint16_t*)w,
+                       Cin, Cout, (uint16_t*)w2, Kp, Np, b, b4);
+  else
+    hipLaunchKernelGGL(vae_subpix_weights_kernel<KH_F16>, dim3(blocks(n, 256)), dim3(256), 0, st, (const uint16_t*)w,
+                       Cin, Cout, (uint16_t*)w2, Kp, Np, b, b4);
+  const hipError_t r = hipGetLastError();
+  return r == hipSuccess ? KH_OK : e.hip(r, "vae_subpix_weights launch");
 }
 
 int vae_pad_weight(hipStream_t st, const void* w, int K, int N, void* out, int Kp, int Np, const float* b, float* bout,

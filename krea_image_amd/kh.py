@@ -31,7 +31,7 @@ SYMBOLS = ["kh_version", "kh_gemm", "kh_attention", "kh_rms_norm", "kh_qk_norm_r
            "kh_gemm_f32", "kh_rope_tables", "kh_dit_layer_forward", "kh_dit_forward",
            "kh_qw_open", "kh_qw_close", "kh_qw_count", "kh_qw_version", "kh_qw_meta", "kh_qw_at", "kh_qw_find",
            "kh_qw_upload", "kh_stream_create", "kh_stream_destroy", "kh_stream_sync", "kh_alloc", "kh_free",
-           "kh_upload", "kh_download", "kh_vae_conv3x3", "kh_vae_im2col", "kh_vae_norm_silu", "kh_vae_unpack", "kh_vae_softmax",
+           "kh_upload", "kh_download", "kh_vae_conv3x3", "kh_vae_subpix_weights", "kh_vae_conv_up2", "kh_vae_im2col", "kh_vae_norm_silu", "kh_vae_unpack", "kh_vae_softmax",
            "kh_vae_conv_out", "kh_vae_workspace_bytes", "kh_vae_decode", "kh_gemm_qk_norm_rope"]
 
 

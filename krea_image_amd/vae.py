@@ -79,8 +79,9 @@ def write_random_vae(path: str, seed: int = 0):
 
 
 def decode_flops(H16: int, W16: int) -> float:
-    """Algorithmic FLOPs of one decode (2 per multiply-add, unpadded channel counts): the convolutions (3 x 3 and
-    1 x 1), the mid-block attention's Q K^T and P V, and the output conv."""
+    """Algorithmic FLOPs of one decode (2 per multiply-add, unpadded channel counts): the convolutions (3 x 3,
+    1 x 1, and the upsamplers in the reference's sub-pixel form: 2 x 2 taps per output pixel), the mid-block
+    attention's Q K^T and P V, and the output conv."""
     P = 4 * H16 * W16
     f = 2.0 * P * 144 * MID  # conv_in
 
@@ -96,7 +97,7 @@ def decode_flops(H16: int, W16: int) -> float:
         cin = cout
         if b < 3:
             P *= 4
-            f += 2.0 * P * 9 * cout * (cout // 2)
+            f += 2.0 * P * 4 * cout * (cout // 2)  # sub-pixel form: 2 x 2 taps per output pixel
             cin = cout // 2
     return f + 2.0 * P * 9 * 96 * 4
 
@@ -110,11 +111,13 @@ def _bind(lib):
     lib.kh_vae_decode.restype = i
     lib.kh_vae_im2col.argtypes = [vp, vp, i, i, i, i, i, i, i, vp, i, cp, i]
     lib.kh_vae_conv3x3.argtypes = [vp, vp, i, i, i, i, i, i, vp, i, i, vp, vp, vp, i, cp, i]
+    lib.kh_vae_subpix_weights.argtypes = [vp, vp, i, i, i, vp, i, i, vp, vp, cp, i]
+    lib.kh_vae_conv_up2.argtypes = [vp, vp, i, i, i, i, i, vp, i, i, vp, vp, i, cp, i]
     lib.kh_vae_norm_silu.argtypes = [vp, vp, i, vp, vp, i, i, i, i, cp, i]
     lib.kh_vae_unpack.argtypes = [vp] * 7 + [i, i, cp, i]
     lib.kh_vae_softmax.argtypes = [vp, vp, i, i, i, ctypes.c_float, vp, cp, i]
     lib.kh_vae_conv_out.argtypes = [vp, vp, i, i, vp, vp, vp, i, i, cp, i]
-    for n in ("kh_vae_conv3x3", "kh_vae_im2col", "kh_vae_norm_silu", "kh_vae_unpack", "kh_vae_softmax", "kh_vae_conv_out"):
+    for n in ("kh_vae_conv3x3", "kh_vae_subpix_weights", "kh_vae_conv_up2", "kh_vae_im2col", "kh_vae_norm_silu", "kh_vae_unpack", "kh_vae_softmax", "kh_vae_conv_out"):
         getattr(lib, n).restype = i
     lib._vae_bound = True
     return lib
@@ -147,6 +150,30 @@ def conv3x3(x, ldx, C, H, W, up, w, K, N, bias, y, ldy, res=None):
     wc = kh.Weight(w).c()
     _call(_bind(kh.load()).kh_vae_conv3x3, kh._stream(), _dp(x), ldx, C, H, W, up, kh.dtype_code(x.dtype),
           ctypes.byref(wc), K, N, _dp(bias), None if res is None else _dp(res), _dp(y), ldy)
+
+
+def subpix_weights(w, Cin, Cout, w2, K, Np, bias=None, bias4=None):
+    """vae_subpix_weights (engine/kernels/vae.metal:134-160): w [9 Cin, Cout] 16-bit -> w2 [K, 4 Np]."""
+    kh._need(w, "w", 9 * Cin, Cout, Cout, 2)
+    kh._need(w2, "w2", K, 4 * Np, 4 * Np, 2)
+    if bias4 is not None:
+        kh._need(bias4, "bias4", 1, 4 * Np, 4 * Np, 4)
+    _call(_bind(kh.load()).kh_vae_subpix_weights, kh._stream(), _dp(w), kh.dtype_code(w.dtype), Cin, Cout, _dp(w2), K,
+          Np, None if bias is None else _dp(bias), None if bias4 is None else _dp(bias4))
+
+
+def conv_up2(x, ldx, C, H, W, w2, K, Np, bias4, y, ldy):
+    """VAEDecoder::conv mode 2 (engine/src/vae.mm:137-150): y [(2H)(2W), ldy] = conv3x3(nearest2x(x)) + bias
+    as four sub-pixel 2 x 2 convs; x [H W, ldx] low-res, w2 / bias4 from subpix_weights."""
+    kh._need(x, "x", H * W, C, ldx, x.element_size())
+    kh._need(w2, "w2", K, 4 * Np, 4 * Np, 2)
+    kh._need(bias4, "bias4", 1, 4 * Np, 4 * Np, 4)
+    kh._need(y, "y", 4 * H * W, Np, ldy, y.element_size())
+    if w2.dtype != x.dtype or y.dtype != x.dtype:
+        raise kh.KhError("conv_up2: x, w2 and y share one 16-bit type")
+    wc = kh.Weight(w2).c()
+    _call(_bind(kh.load()).kh_vae_conv_up2, kh._stream(), _dp(x), ldx, C, H, W, kh.dtype_code(x.dtype),
+          ctypes.byref(wc), K, Np, _dp(bias4), _dp(y), ldy)
 
 
 def im2col(x, ldx, C, H, W, up, m0, rows, col, Kpad):

@@ -238,6 +238,45 @@ def vae_conv(x, H, W, w, bias, N, ks=3, up=0, res=None):
     return y
 
 
+def vae_subpix_weights(w, Cin, Cout):
+    """Sub-pixel weights of nearest-2x + 3x3 (engine/kernels/vae.metal:134-160): W2 [4 Cin, 4 Cout] bf16 bits,
+    W2[(2r + s) Cin + ci, (2py + px) Cout + co] = bf16(fp32 sum, in (ky, kx) order, of the taps W[ky, kx] with
+    ky in [0, py] for r = 0 and [1 + py, 2] for r = 1, kx likewise)."""
+    wf = to_f32(np.asarray(w, np.uint16), BF16).reshape(3, 3, Cin, Cout)
+    W2 = np.zeros((4 * Cin, 4 * Cout), np.float32)
+    for ph in range(4):
+        py, px = ph >> 1, ph & 1
+        for t in range(4):
+            r, sc = t >> 1, t & 1
+            y0, y1 = (1 + py, 2) if r else (0, py)
+            x0, x1 = (1 + px, 2) if sc else (0, px)
+            acc = np.zeros((Cin, Cout), np.float32)
+            for ky in range(y0, y1 + 1):
+                for kx in range(x0, x1 + 1):
+                    acc = acc + wf[ky, kx]
+            W2[t * Cin:(t + 1) * Cin, ph * Cout:(ph + 1) * Cout] = acc
+    return from_f32(W2, BF16)
+
+
+def vae_conv_up2(x, H, W, w2, bias, Cout):
+    """conv3x3(nearest2x(x)) as four 2x2 sub-pixel convs (engine/src/vae.mm:137-150, vconv mode 2): x [H W, Cin]
+    bf16 low-res, w2 from vae_subpix_weights, bias [Cout] f32 -> y [(2H)(2W), Cout] bf16. Phase (py, px) is a
+    3x3 conv of x whose taps at offsets (r + py - 1, s + px - 1) hold W2's 2x2 taps and the rest are zero."""
+    x = np.ascontiguousarray(x, np.uint16)
+    Cin = x.shape[1]
+    w2 = np.asarray(w2, np.uint16)
+    y = np.empty((2 * H, 2 * W, Cout), np.uint16)
+    for ph in range(4):
+        py, px = ph >> 1, ph & 1
+        k3 = np.zeros((3, 3, Cin, Cout), np.uint16)
+        for t in range(4):
+            r, sc = t >> 1, t & 1
+            k3[r + py, sc + px] = w2[t * Cin:(t + 1) * Cin, ph * Cout:(ph + 1) * Cout]
+        yp = vae_conv(x, H, W, k3.reshape(9 * Cin, Cout), bias, Cout, ks=3)
+        y[py::2, px::2] = yp.reshape(H, W, Cout)
+    return y.reshape(4 * H * W, Cout)
+
+
 def vae_norm_silu(x, gamma, silu=1):
     x = np.ascontiguousarray(x, np.uint16)
     y = np.empty_like(x)

@@ -77,3 +77,36 @@ def test_conv3x3_rejects_bad_arguments(dev):
         vae.conv3x3(x, 24, 20, 8, 8, 0, w, 256, 64, b, y, 64)   # C % 8
     with pytest.raises(kh.KhError, match="even"):
         vae.conv3x3(x, 24, 24, 7, 8, 1, w, 256, 64, b, y, 64)   # odd upsampled size
+
+
+@pytest.mark.parametrize("H,W,C,Cout", [(5, 7, 16, 96), (12, 20, 384, 192), (30, 34, 192, 96), (16, 24, 96, 384)])
+def test_conv_up2_subpixel(dev, H, W, C, Cout):
+    """The upsampling conv as four sub-pixel 2x2 convs (the reference's mode 2): folded weights bit-exact
+    against the oracle's restatement, the conv against the oracle's sub-pixel conv and, to the folding's
+    bf16 rounding, against the direct 3x3 conv of the upsampled image."""
+    from krea_image_amd import vae
+    print(f"[vae conv_up2] H={H} W={W} C={C} Cout={Cout}", flush=True)
+    rng = np.random.default_rng(7 * H + C)
+    Np = (Cout + 63) // 64 * 64
+    x = _bf(rng.standard_normal((H * W, C)))
+    w = _bf(rng.standard_normal((9 * C, Cout)) / np.sqrt(9 * C))
+    bias = (rng.standard_normal(Cout) * 0.1).astype(np.float32)
+    K = (4 * C + 63) // 64 * 64
+    wd, bd, xd = _dev16(w, dev), torch.from_numpy(bias).to(dev), _dev16(x, dev)
+    w2 = torch.empty(K, 4 * Np, dtype=torch.bfloat16, device=dev)
+    b4 = torch.empty(4 * Np, device=dev)
+    vae.subpix_weights(wd, C, Cout, w2, K, Np, bd, b4)
+    y = torch.empty(4 * H * W, Np, dtype=torch.bfloat16, device=dev)
+    vae.conv_up2(xd, C, C, H, W, w2, K, Np, b4, y, Np)
+    torch.cuda.synchronize()
+    ref_w2 = O.vae_subpix_weights(w, C, Cout)
+    got_w2 = w2.view(torch.int16).cpu().numpy().view(np.uint16)
+    for ph in range(4):
+        np.testing.assert_array_equal(got_w2[:4 * C, ph * Np:ph * Np + Cout], ref_w2[:, ph * Cout:(ph + 1) * Cout])
+        assert not got_w2[:, ph * Np + Cout:(ph + 1) * Np].any() and not got_w2[4 * C:].any()
+    np.testing.assert_array_equal(b4.cpu().numpy().reshape(4, Np)[:, :Cout], np.tile(bias, (4, 1)))
+    g = O.to_f32(y.view(torch.int16).cpu().numpy().view(np.uint16)[:, :Cout], O.BF16)
+    ref = O.to_f32(O.vae_conv_up2(x, H, W, ref_w2, bias, Cout), O.BF16)
+    assert np.linalg.norm(g - ref) / np.linalg.norm(ref) < 5e-3
+    direct = O.to_f32(O.vae_conv(x, 2 * H, 2 * W, w, bias, Cout, ks=3, up=1), O.BF16)
+    assert np.linalg.norm(g - direct) / np.linalg.norm(direct) < 2e-2

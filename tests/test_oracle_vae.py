@@ -133,3 +133,32 @@ def test_vae_conv_more_than_1024_outputs():
     got = f32(O.vae_conv(x, 1, P, w, b, N, ks=1))
     ref = f32(x) @ f32(w) + b
     assert np.abs(got - ref).max() <= 2 ** -8 * np.abs(ref).max()
+
+
+def test_vae_subpix_weights_closed_form():
+    """Each folded tap is the sum of the 3x3 taps that the nearest upsample maps onto it: every 3x3 tap is used
+    exactly once per phase, so the four 2x2 taps of a phase add up to the sum of all nine (up to rounding)."""
+    rng = np.random.default_rng(4)
+    Cin, Cout = 8, 16
+    w = O.from_f32(rng.standard_normal((9 * Cin, Cout)).astype(np.float32), O.BF16)
+    w2 = O.to_f32(O.vae_subpix_weights(w, Cin, Cout), O.BF16)
+    wf = O.to_f32(w, O.BF16).reshape(3, 3, Cin, Cout)
+    # phase (0, 0), tap (0, 0) is the single corner tap W[0, 0]; tap (1, 1) sums W[1:, 1:]
+    np.testing.assert_array_equal(w2[:Cin, :Cout], wf[0, 0])
+    np.testing.assert_allclose(w2[3 * Cin:4 * Cin, :Cout], wf[1:, 1:].sum((0, 1)), rtol=1e-2, atol=1e-2)
+    for ph in range(4):
+        tot = w2[:, ph * Cout:(ph + 1) * Cout].reshape(4, Cin, Cout).sum(0)
+        np.testing.assert_allclose(tot, wf.sum((0, 1)), rtol=3e-2, atol=3e-2)
+
+
+def test_vae_conv_up2_matches_direct_upsampled_conv():
+    """conv3x3(nearest2x(x)) == the sub-pixel form exactly in real arithmetic; here the folded weights are
+    rounded to bf16 once, so the two agree to a few bf16 ulps."""
+    rng = np.random.default_rng(5)
+    H, W, Cin, Cout = 5, 6, 16, 8
+    x = O.from_f32(rng.standard_normal((H * W, Cin)).astype(np.float32), O.BF16)
+    w = O.from_f32((rng.standard_normal((9 * Cin, Cout)) / 12).astype(np.float32), O.BF16)
+    b = rng.standard_normal(Cout).astype(np.float32)
+    direct = O.to_f32(O.vae_conv(x, 2 * H, 2 * W, w, b, Cout, ks=3, up=1), O.BF16)
+    sub = O.to_f32(O.vae_conv_up2(x, H, W, O.vae_subpix_weights(w, Cin, Cout), b, Cout), O.BF16)
+    assert np.linalg.norm(sub - direct) / np.linalg.norm(direct) < 1e-2

@@ -1,6 +1,7 @@
 """The oracle's composition of VAEDecoder::run (engine/src/vae.mm:289-337) over a vae.qw file read on the host:
 the decoder graph of krea_image_amd/vae.py built from oracle/oracle.c's per-op restatements (or_vae_*), with the
-mid-block attention (vae.mm:245-270) as numpy f32 Q K^T + the oracle's row softmax + P V rounded to bf16.
+mid-block attention (vae.mm:245-270) as numpy f32 Q K^T + the oracle's row softmax + P V rounded to bf16, and
+the upsamplers as the reference's sub-pixel convs (vae.mm:137-150).
 Test infrastructure only."""
 import numpy as np
 
@@ -48,7 +49,8 @@ def decode(f, z, H16, W16):
             x = _resblock(f, x, H, W, f"{d}up_blocks.{b}.resnets.{r}.", cout)
         if b < 3:
             u = f"{d}up_blocks.{b}.upsamplers.0.resample.1."
+            w2 = O.vae_subpix_weights(f.array(u + "weight"), cout, cout // 2)
+            x = O.vae_conv_up2(x, H, W, w2, f.array(u + "bias"), cout // 2)  # the reference's mode 2
             H, W = 2 * H, 2 * W
-            x = O.vae_conv(x, H, W, f.array(u + "weight"), f.array(u + "bias"), cout // 2, up=1)
     x = O.vae_norm_silu(x, f.array(d + "norm_out.gamma"), 1)
     return O.vae_conv_out(x, f.array(d + "conv_out.weight"), f.array(d + "conv_out.bias"), H, W).reshape(H, W, 4)
