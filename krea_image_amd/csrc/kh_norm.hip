@@ -186,15 +186,18 @@ __global__ void gemv_init(float* y, const float* bias, int rows, int N, int ldy,
   }
 }
 
-template <int WF>  // 0: 16-bit weights (8 columns per lane), 1: int8 per-channel, 2: int8 group (16 per lane)
+// WF 0: 16-bit weights (8 columns per lane), 1: int8 per-channel, 2: int8 group (16 per lane); RMAX: rows the
+// instantiation handles (1: the DiT's single conditioning vector, 4: up to four; sizes the accumulators and the
+// partial-sum LDS, so the one-row form fits four times as many workgroups per CU)
+template <int WF, int RMAX>
 __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, const void* __restrict__ W,
                                                    const void* __restrict__ S, int s_dtype, int group, int w16_dtype,
                                                    float* __restrict__ y, int rows, int N, int K, int ldw, int ldy,
                                                    int silu, int kchunk) {
   constexpr int CPL = WF == 0 ? 8 : 16;  // columns per lane
   constexpr int COLS = 16 * CPL;         // 16 lanes span the block's columns; lane >> 4 picks a row group
-  __shared__ float xs[4][512];           // activated x of this slab (rows x kchunk), kchunk <= 512
-  __shared__ float part[16][4][COLS];    // [row group][row][column]
+  __shared__ float xs[RMAX][512];        // activated x of this slab (rows x kchunk), kchunk <= 512
+  __shared__ float part[16][RMAX][COLS]; // [row group][row][column]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int rg = wave * 4 + (lane >> 4);  // 16 row groups
   const int n = blockIdx.x * COLS + (lane & 15) * CPL;
@@ -205,9 +208,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
     xs[r][k] = silu ? silu_f(v) : v;
   }
   __syncthreads();
-  float acc[4][CPL];
+  float acc[RMAX][CPL];
 #pragma unroll
-  for (int r = 0; r < 4; r++)
+  for (int r = 0; r < RMAX; r++)
 #pragma unroll
     for (int c = 0; c < CPL; c++) acc[r][c] = 0.f;
   if (n < N) {
@@ -241,7 +244,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
           }
         }
 #pragma unroll
-        for (int r = 0; r < 4; r++) {  // static indices keep acc in registers
+        for (int r = 0; r < RMAX; r++) {  // static indices keep acc in registers
           if (r >= rows) break;
           const float xv = xs[r][k - k0];
 #pragma unroll
@@ -251,7 +254,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
     }
   }
 #pragma unroll
-  for (int r = 0; r < 4; r++) {
+  for (int r = 0; r < RMAX; r++) {
     if (r >= rows) break;
 #pragma unroll
     for (int c = 0; c < CPL; c++) part[rg][r][(lane & 15) * CPL + c] = acc[r][c];
@@ -424,25 +427,32 @@ int gemv(hipStream_t st, const float* x, const kh_weight& W, float* y, int rows,
   } else {
     return e.fail("gemv: weight dtype must be int8, f16 or bf16");
   }
-  // K split so the grid has >= ~512 workgroups; each slab's x fits the 512-entry LDS stage
+  // K split so the grid has >= wg_target workgroups; each slab's x fits the 512-entry LDS stage
   const int cols = wf == 0 ? 128 : 256;
   if (N % (wf == 0 ? 8 : 16) || ldw % 16) return e.fail("gemv: N must be a multiple of 16 (8 for 16-bit), ldw of 16");
   const int col_blocks = (N + cols - 1) / cols;
   int ksplit = 1;
-  while (ksplit < GEMV_KSPLIT_MAX && (col_blocks * ksplit < 512 || (K + ksplit - 1) / ksplit > 512)) ksplit *= 2;
+  // one-row calls fit six workgroups per CU: more K splits keep more loads in flight (measured at 3072 ->
+  // 18432 int8: 512 workgroups 15.1 us, 1024 13.8 us, 2048 14.5 us)
+  const int wg_target = rows == 1 ? 1024 : 512;
+  while (ksplit < GEMV_KSPLIT_MAX && (col_blocks * ksplit < wg_target || (K + ksplit - 1) / ksplit > 512)) ksplit *= 2;
   const int kchunk = (K + ksplit - 1) / ksplit;
   if (kchunk > 512) return e.fail("gemv: K %d too large", K);
   hipLaunchKernelGGL(gemv_init, dim3((N + 255) / 256), dim3(256), 0, st, y, bias, rows, N, N, (act & 2) ? 1 : 0);
   dim3 grid(col_blocks, (K + kchunk - 1) / kchunk), block(256);
-  if (wf == 0)
-    hipLaunchKernelGGL(gemv_kernel<0>, grid, block, 0, st, x, W.w, W.s, W.s_dtype, group, W.w_dtype, y, rows, N, K,
-                       ldw, N, act & 1, kchunk);
-  else if (wf == 1)
-    hipLaunchKernelGGL(gemv_kernel<1>, grid, block, 0, st, x, W.w, W.s, W.s_dtype, group, W.w_dtype, y, rows, N, K,
-                       ldw, N, act & 1, kchunk);
-  else
-    hipLaunchKernelGGL(gemv_kernel<2>, grid, block, 0, st, x, W.w, W.s, W.s_dtype, group, W.w_dtype, y, rows, N, K,
-                       ldw, N, act & 1, kchunk);
+#define KH_GEMV(WF_, R_)                                                                                      \
+  hipLaunchKernelGGL((gemv_kernel<WF_, R_>), grid, block, 0, st, x, W.w, W.s, W.s_dtype, group, W.w_dtype, y, rows, \
+                     N, K, ldw, N, act & 1, kchunk)
+  if (rows == 1) {
+    if (wf == 0) KH_GEMV(0, 1);
+    else if (wf == 1) KH_GEMV(1, 1);
+    else KH_GEMV(2, 1);
+  } else {
+    if (wf == 0) KH_GEMV(0, 4);
+    else if (wf == 1) KH_GEMV(1, 4);
+    else KH_GEMV(2, 4);
+  }
+#undef KH_GEMV
   const hipError_t r = hipGetLastError();
   return r == hipSuccess ? KH_OK : e.hip(r, "gemv launch");
 }
