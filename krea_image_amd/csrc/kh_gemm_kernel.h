@@ -440,7 +440,6 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
     }
     // sum = p_c0 + p_c0+1 + ... in K order (own partial re-read like the others, so the association does
     // not depend on which workgroup arrived last); 8 quads per batch of loads
-    static_assert(IB * 4 == 8, "fix-up batches assume 8 accumulator quads per jb");
 #pragma unroll
     for (int jb = 0; jb < 4; jb++)
 #pragma unroll
@@ -448,14 +447,16 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
     for (int c = c0; c <= c1; c++) {
       const float* src = slot(c);
 #pragma unroll
-      for (int jb = 0; jb < 4; jb++) {
-        f32x4 v[8];
-        ld_coherent_8x_b128(src + (size_t)jb * 8 * (NTHR * 4), NTHR * 4, v);
+      for (int jb = 0; jb < 4; jb++)
 #pragma unroll
-        for (int u = 0; u < 8; u++)
+        for (int u0 = 0; u0 < IB * 4; u0 += 8) {  // 8 accumulator quads per batch of loads
+          f32x4 v[8];
+          ld_coherent_8x_b128(src + (size_t)(jb * IB * 4 + u0) * (NTHR * 4), NTHR * 4, v);
 #pragma unroll
-          for (int e = 0; e < 4; e++) acc[jb][u >> 2][4 * (u & 3) + e] += v[u][e];
-      }
+          for (int u = 0; u < 8; u++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[jb][(u0 + u) >> 2][4 * ((u0 + u) & 3) + e] += v[u][e];
+        }
     }
     if (tid == 0) __hip_atomic_store(p.cnt + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next launch
   }
