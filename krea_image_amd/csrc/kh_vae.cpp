@@ -6,6 +6,7 @@
 // everything is enqueued on one stream.
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <string>
 
 #include "kh_internal.h"
@@ -16,13 +17,25 @@ namespace {
 
 constexpr int OUTS[4] = {384, 384, 192, 96};  // up-block output channels (vae.mm:319)
 constexpr int MID_C = 384;
-constexpr int QC = 2048;                       // attention query rows per S chunk
+constexpr long long S_CHUNK_BYTES = 1LL << 30;  // attention: f32 S chunk budget (query rows x padded keys)
 
 inline long long ru(long long v, long long a) { return (v + a - 1) / a * a; }
 inline int ld_of(int C) { return (int)ru(C, 64); }  // GEMM outputs are padded to 64 columns
 
+// Query rows per attention S chunk: all of them while S fits S_CHUNK_BYTES (16384 at 1024^2), else a multiple of
+// 256 (at least 256). Few, tall chunks keep the P V GEMM (rows x 384 outputs, K = all keys) wide enough that
+// stream-K splits each tile only a few ways. KH_VAE_QCHUNK overrides (tests of the multi-chunk path).
+long long query_chunk(long long P0, long long Pp0) {
+  if (const char* e = getenv("KH_VAE_QCHUNK")) {
+    const long long q = atoll(e);
+    if (q > 0) return std::min(q, P0);
+  }
+  const long long fit = std::max<long long>(256, S_CHUNK_BYTES / (4 * Pp0) / 256 * 256);
+  return std::min(fit, P0);
+}
+
 struct Plan {
-  long long P0, P3, Pp0;  // VAE-input pixels, output pixels, P0 rounded up to 64
+  long long P0, P3, Pp0, qc;  // VAE-input pixels, output pixels, P0 rounded up to 64, attention query chunk
   size_t act, wpad, bpad, qkv, kt, S, Pm, total;
   size_t off_act[5], off_wpad, off_bpad, off_qkv, off_kt, off_S, off_Pm;
 };
@@ -40,9 +53,9 @@ Plan plan(int H16, int W16) {
   p.bpad = (size_t)ru(4 * 1152 * 4, 256);
   p.qkv = (size_t)ru(p.Pp0 * 3 * MID_C * 2, 256);
   p.kt = (size_t)ru((long long)MID_C * p.Pp0 * 2, 256);
-  const long long qc = std::min<long long>(QC, p.P0);
-  p.S = (size_t)ru(qc * p.Pp0 * 4, 256);
-  p.Pm = (size_t)ru(qc * p.Pp0 * 2, 256);
+  p.qc = query_chunk(p.P0, p.Pp0);
+  p.S = (size_t)ru(p.qc * p.Pp0 * 4, 256);
+  p.Pm = (size_t)ru(p.qc * p.Pp0 * 2, 256);
   size_t off = 0;
   for (int i = 0; i < 5; i++) {
     p.off_act[i] = off;
@@ -223,8 +236,8 @@ class Decoder {
     const kh_weight wk{kt, nullptr, KH_BF16, KH_F32, 0};
     const kh_weight wv{qkv + 2 * C, nullptr, KH_BF16, KH_F32, 0};
     const float scale = (float)(1.0 / std::sqrt((double)C));
-    for (long long q0 = 0; q0 < P; q0 += QC) {
-      const int rows = (int)std::min<long long>(QC, P - q0);
+    for (long long q0 = 0; q0 < P; q0 += pl_.qc) {
+      const int rows = (int)std::min<long long>(pl_.qc, P - q0);
       if ((rc = gemm(st_, KH_EPI_F32, qkv + (size_t)q0 * 3 * C, KH_BF16, wk, S, rows, (int)Pp, C, 3 * C, (int)Pp, (int)Pp,
                      nullptr, e_)))
         return rc;

@@ -121,6 +121,55 @@ __global__ __launch_bounds__(256) void vae_norm_silu_kernel(const uint16_t* __re
   }
 }
 
+// Register variant for C = 24 L channels with L in {4, 8, 16} (the decoder's 96, 192 and 384): L lanes per
+// pixel, 3 chunks of 8 channels per lane (lane q holds chunks q, q + L, q + 2L: consecutive lanes read
+// consecutive 16 bytes), so x is read once and every lane is busy; same arithmetic as above.
+template <int L>
+__global__ __launch_bounds__(256) void vae_norm_silu_reg_kernel(const uint16_t* __restrict__ x, int ldx,
+                                                               const float* __restrict__ gamma,
+                                                               uint16_t* __restrict__ y, int ldy, int P, int silu) {
+  constexpr int CPL = 3, C = 8 * CPL * L;
+  const int q = threadIdx.x % L;
+  const int pix0 = blockIdx.x * (256 / L) + threadIdx.x / L;
+  const bool valid = pix0 < P;
+  const int pix = valid ? pix0 : P - 1;
+  const uint16_t* xr = x + (size_t)pix * ldx;
+  u32x4v v[CPL];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < CPL; j++) {
+    v[j] = *(const u32x4v*)(xr + (q + L * j) * 8);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const float a = bf((uint16_t)v[j][k]), b = bf((uint16_t)(v[j][k] >> 16));
+      ss += a * a + b * b;
+    }
+  }
+#pragma unroll
+  for (int o = L / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, L);
+  const float scale = sqrtf((float)C) / fmaxf(sqrtf(ss), 1e-12f);
+  if (!valid) return;
+  uint16_t* yr = y + (size_t)pix * ldy;
+#pragma unroll
+  for (int j = 0; j < CPL; j++) {
+    const int c = q + L * j;
+    const f32x4 g0 = *(const f32x4*)(gamma + c * 8), g1 = *(const f32x4*)(gamma + c * 8 + 4);
+    const float g[8] = {g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
+    u32x4v o;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      float a = bf((uint16_t)v[j][k]) * scale * g[2 * k];
+      float b = bf((uint16_t)(v[j][k] >> 16)) * scale * g[2 * k + 1];
+      if (silu) {
+        a = silu_f(a);
+        b = silu_f(b);
+      }
+      o[k] = pack16<KH_BF16>(a, b);
+    }
+    *(u32x4v*)(yr + c * 8) = o;
+  }
+}
+
 // ---- y[i] += a[i] (bf16, n elements, n % 8 == 0): the residual of the resblocks / attention ----
 __global__ __launch_bounds__(256) void vae_add_kernel(uint16_t* __restrict__ y, const uint16_t* __restrict__ a,
                                                      long long n8) {
@@ -175,6 +224,68 @@ __global__ __launch_bounds__(256) void vae_softmax_kernel(const float* __restric
   const float inv = 1.0f / (red[0] + red[1] + red[2] + red[3]);
   uint16_t* o = Pm + (size_t)blockIdx.x * ld;
   for (int i = tid; i < n; i += 256) o[i] = to16<KH_BF16>(__expf(s[i] * scale - mx) * inv);
+}
+
+// One-read variant for rows of up to 1024 NV values (the mid block's 16384 keys at 1024^2: NV = 16): each
+// thread keeps its 4 NV values (float4 loads, 16 KB apart across the workgroup) in registers through the max,
+// sum and store phases, so S is read once instead of three times. Needs ld % 4 == 0 and 16-byte aligned S,
+// 8-byte aligned Pm.
+template <int NV>
+__global__ __launch_bounds__(256) void vae_softmax_rows_kernel(const float* __restrict__ S, int ld, int n, float scale,
+                                                              uint16_t* __restrict__ Pm) {
+  __shared__ float red[2][4];
+  const float* s = S + (size_t)blockIdx.x * ld;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  f32x4 v[NV];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    const int i = 4 * (tid + 256 * j);
+    if (i + 3 < n) {
+      v[j] = *(const f32x4*)(s + i);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; e++) v[j][e] = i + e < n ? s[i + e] : -INFINITY;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      v[j][e] *= scale;
+      mx = fmaxf(mx, v[j][e]);
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if (lane == 0) red[0][wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+  float sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; j++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      v[j][e] = __expf(v[j][e] - mx);  // padding: exp(-inf) = 0
+      sum += v[j][e];
+    }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+  if (lane == 0) red[1][wave] = sum;
+  __syncthreads();
+  const float inv = 1.0f / (red[1][0] + red[1][1] + red[1][2] + red[1][3]);
+  uint16_t* o = Pm + (size_t)blockIdx.x * ld;
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    const int i = 4 * (tid + 256 * j);
+    uint16_t h[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) h[e] = to16<KH_BF16>(v[j][e] * inv);
+    if (i + 3 < n) {
+      *(uint2*)(o + i) = make_uint2(h[0] | (uint32_t)h[1] << 16, h[2] | (uint32_t)h[3] << 16);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        if (i + e < n) o[i + e] = h[e];
+    }
+  }
 }
 
 // ---- final 3 x 3 conv C -> 4 (RGBA; alpha's weights are zero and its bias 1) + clamp(-1, 1) + [0, 255]
@@ -320,8 +431,19 @@ int vae_norm_silu(hipStream_t st, const void* x, int ldx, const float* gamma, vo
   if (P <= 0 || C <= 0 || C % 8 || ldx < C || ldy < C || ldx % 8 || ldy % 8)
     return e.fail("vae_norm_silu: bad shape P=%d C=%d ldx=%d ldy=%d", P, C, ldx, ldy);
   if (((uintptr_t)x | (uintptr_t)y) & 15) return e.fail("vae_norm_silu: 16-byte alignment");
-  hipLaunchKernelGGL(vae_norm_silu_kernel, dim3(blocks(P, 16)), dim3(256), 0, st, (const uint16_t*)x, ldx, gamma,
-                     (uint16_t*)y, ldy, P, C, silu);
+  const bool g16 = !((uintptr_t)gamma & 15);
+  if (g16 && C == 96)
+    hipLaunchKernelGGL(vae_norm_silu_reg_kernel<4>, dim3(blocks(P, 64)), dim3(256), 0, st, (const uint16_t*)x, ldx,
+                       gamma, (uint16_t*)y, ldy, P, silu);
+  else if (g16 && C == 192)
+    hipLaunchKernelGGL(vae_norm_silu_reg_kernel<8>, dim3(blocks(P, 32)), dim3(256), 0, st, (const uint16_t*)x, ldx,
+                       gamma, (uint16_t*)y, ldy, P, silu);
+  else if (g16 && C == 384)
+    hipLaunchKernelGGL(vae_norm_silu_reg_kernel<16>, dim3(blocks(P, 16)), dim3(256), 0, st, (const uint16_t*)x, ldx,
+                       gamma, (uint16_t*)y, ldy, P, silu);
+  else
+    hipLaunchKernelGGL(vae_norm_silu_kernel, dim3(blocks(P, 16)), dim3(256), 0, st, (const uint16_t*)x, ldx, gamma,
+                       (uint16_t*)y, ldy, P, C, silu);
   const hipError_t r = hipGetLastError();
   return r == hipSuccess ? KH_OK : e.hip(r, "vae_norm_silu launch");
 }
@@ -348,7 +470,11 @@ int vae_transpose(hipStream_t st, const void* in, int ld, int off, int P, int C,
 int vae_softmax(hipStream_t st, const float* S, int ld, int rows, int n, float scale, void* Pm, Err& e) {
   if (!S || !Pm) return e.fail("vae_softmax: null pointer");
   if (rows <= 0 || n <= 0 || n > ld) return e.fail("vae_softmax: bad shape rows=%d n=%d ld=%d", rows, n, ld);
-  hipLaunchKernelGGL(vae_softmax_kernel, dim3(rows), dim3(256), 0, st, S, ld, n, scale, (uint16_t*)Pm);
+  constexpr int NV = 16;
+  if (n <= 1024 * NV && ld % 4 == 0 && !((uintptr_t)S & 15) && !((uintptr_t)Pm & 7))
+    hipLaunchKernelGGL(vae_softmax_rows_kernel<NV>, dim3(rows), dim3(256), 0, st, S, ld, n, scale, (uint16_t*)Pm);
+  else
+    hipLaunchKernelGGL(vae_softmax_kernel, dim3(rows), dim3(256), 0, st, S, ld, n, scale, (uint16_t*)Pm);
   const hipError_t r = hipGetLastError();
   return r == hipSuccess ? KH_OK : e.hip(r, "vae_softmax launch");
 }

@@ -54,7 +54,8 @@ def test_im2col_exact(dev, up):
     np.testing.assert_array_equal(_host16(col), ref)
 
 
-@pytest.mark.parametrize("C,silu", [(96, 1), (384, 0), (8, 1)])
+# 96 / 192 / 384: the register kernel (4, 8, 16 lanes per pixel); 8 and 104: the generic one
+@pytest.mark.parametrize("C,silu", [(96, 1), (96, 0), (192, 1), (384, 0), (384, 1), (8, 1), (104, 1)])
 def test_norm_silu(dev, C, silu):
     from krea_image_amd import vae
     rng = np.random.default_rng(C)
@@ -88,11 +89,12 @@ def test_unpack(dev):
     assert np.abs(got - ref).max() <= 2 ** -7 * np.abs(ref).max()
 
 
-@pytest.mark.parametrize("n", [1, 100, 4099])
-def test_softmax(dev, n):
+# ld % 4 != 0: the three-pass kernel; ld % 4 == 0 and n <= 16384: the one-read kernel (ragged tail, full rows)
+@pytest.mark.parametrize("n,ld", [(1, 62), (100, 161), (4099, 4160), (16384, 16384), (13, 16), (16385, 16448)])
+def test_softmax(dev, n, ld):
     from krea_image_amd import vae
     rng = np.random.default_rng(n)
-    rows, ld = 9, n + 61
+    rows = 9
     S = (rng.standard_normal((rows, ld)) * 6).astype(np.float32)
     Pm = torch.zeros((rows, ld), dtype=torch.int16, device=dev)
     print(f"[vae softmax] rows={rows} n={n} ld={ld}", flush=True)
@@ -130,13 +132,16 @@ def vae_file(tmp_path_factory, dev):
     f.close()
 
 
-# 2 x 2: 16 mid pixels, keys padded to 64; 4 x 4: 64 pixels, no padding; 24 x 24: 2304 pixels, two query chunks
-@pytest.mark.parametrize("H16,W16", [(2, 2), (4, 4), (3, 5), (24, 24)])
-def test_decode_matches_oracle(dev, vae_file, H16, W16):
+# 2 x 2: 16 mid pixels, keys padded to 64; 4 x 4: 64 pixels, no padding; 24 x 24: 2304 pixels, one query chunk
+# by default, three of 768 rows with KH_VAE_QCHUNK (the multi-chunk path of larger images)
+@pytest.mark.parametrize("H16,W16,qchunk", [(2, 2, None), (4, 4, None), (3, 5, None), (24, 24, None), (24, 24, 768)])
+def test_decode_matches_oracle(dev, vae_file, H16, W16, qchunk, monkeypatch):
     from krea_image_amd import vae
+    if qchunk:
+        monkeypatch.setenv("KH_VAE_QCHUNK", str(qchunk))
     rng = np.random.default_rng(H16 * 100 + W16)
     z = rng.standard_normal((H16 * W16, 64)).astype(np.float32)
-    print(f"[vae decode] latent {H16}x{W16} -> {16 * H16}x{16 * W16}", flush=True)
+    print(f"[vae decode] latent {H16}x{W16} -> {16 * H16}x{16 * W16} qchunk={qchunk}", flush=True)
     dec = vae.VaeDecoder(vae_file, dev)
     zt = torch.from_numpy(z).to(dev)
     got = dec.decode(zt, H16, W16)
