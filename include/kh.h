@@ -26,7 +26,7 @@ typedef void* kh_stream; /* hipStream_t */
 enum { KH_OK = 0, KH_EINVAL = -1, KH_EHIP = -2 };
 
 /* element types */
-enum { KH_F32 = 0, KH_F16 = 1, KH_BF16 = 2, KH_I8 = 3 };
+enum { KH_F32 = 0, KH_F16 = 1, KH_BF16 = 2, KH_I8 = 3, KH_I8P = 4 /* int8 in kh_pack_int8's layout */ };
 
 /* GEMM epilogues: engine/src/metal.h:37-38 (enum class Epi) and engine/kernels/gemm.metal:28-37.
  * "16" outputs use the activation type (bf16 in the reference engine, fp16 in the benchmark configs). */
@@ -49,6 +49,8 @@ enum {
  *       reference's dit_q8.qw, tools/convert.py:92-99).
  *   w_dtype KH_I8, group == K: per-output-channel scales s[N] (fp16 or f32), applied to the fp32
  *       accumulator (q is exact in fp16/bf16), the format of tools/build_ane.py:79-80.
+ *   w_dtype KH_I8P: int8 as KH_I8 (per-channel scales, or group scales in f32), rearranged by kh_pack_int8;
+ *       same results as KH_I8, bitwise. kh_gemm and kh_gemm_qk_norm_rope only (not kh_gemv).
  * s_dtype: KH_F32, KH_F16 or KH_BF16. */
 typedef struct kh_weight {
   const void* w;
@@ -74,6 +76,15 @@ typedef struct kh_weight {
  * Replaces krea::Metal::gemm (engine/src/metal.h:66-69, engine/src/metal.mm:146-163). */
 int kh_gemm(kh_stream stream, int epi, const void* A, int a_dtype, const kh_weight* W, void* C, int M, int N, int K,
             int lda, int ldw, int ldc, const void* vec, char* err, int errlen);
+
+/* Load-time rearrangement of int8 weights Wt[K, ldw] (row stride ldw bytes) into the packed layout kh_gemm reads
+ * as w_dtype KH_I8P: element (k, n) at byte (k / 8) 8 ldw + 32 (n / 4) + 4 (k % 8) + n % 4, i.e. 8-row panels in
+ * which each 4-column group's 8 x 4 bytes are contiguous. A GEMM thread loads one such group per K step (two
+ * 16-byte loads instead of eight 4-byte row loads; the bytes it receives are the same). Column views keep
+ * working: columns [c0, c0 + N) with c0 % 4 == 0 start at byte 8 c0 of the packed buffer, with the same ldw.
+ * K % 8 == 0, ldw % 16 == 0; out holds K ldw bytes and must not overlap W. No counterpart in the reference
+ * (its Metal kernels read the input-major layout of tools/convert.py directly). */
+int kh_pack_int8(kh_stream stream, const void* W, int K, int ldw, void* out, char* err, int errlen);
 
 /* Flash attention, head dim 128: O[q, h] = softmax_k(Q[q,h] . K[k, h/group] / sqrt(128) (+ QB[q,h] KB[k,h/group]))
  * V[k, h/group] (* sigmoid(G[q, h]) if G), fp32 scores / softmax / accumulation, P rounded to the 16-bit type

@@ -13,6 +13,12 @@ int kh_gemm(kh_stream stream, int epi, const void* A, int a_dtype, const kh_weig
   return kh::gemm((hipStream_t)stream, epi, A, a_dtype, *W, C, M, N, K, lda, ldw, ldc, vec, e);
 }
 
+int kh_pack_int8(kh_stream stream, const void* W, int K, int ldw, void* out, char* err, int errlen) {
+  kh::Err e{err, errlen};
+  e.clear();
+  return kh::pack_int8((hipStream_t)stream, W, K, ldw, out, e);
+}
+
 int kh_attention(kh_stream stream, const void* Q, const void* K, const void* V, void* O, int dtype, int Lq, int Lk,
                  int heads, int ldq, int ldk, int ldv, int ldo, int group, int causal, int q_pos0, const void* G,
                  int ldg, const float* QB, const float* KB, char* err, int errlen) {

@@ -87,6 +87,11 @@ __device__ __forceinline__ u32x2 vm_load_b64(const void* p) {
   asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(r) : "v"(p));
   return r;
 }
+__device__ __forceinline__ u32x4 vm_load_b128(const void* p) {
+  u32x4 r;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p));
+  return r;
+}
 __device__ __forceinline__ uint32_t vm_load_u16(const void* p) {
   uint32_t r;
   asm volatile("global_load_ushort %0, %1, off" : "=v"(r) : "v"(p));

@@ -164,7 +164,7 @@ int gemm_run(hipStream_t st, int epi, const void* A, int a_dtype, const kh_weigh
   if (needs_vec && !vec) return e.fail("gemm: epilogue %d needs vec", epi);
   int wf;
   int group = 0;
-  if (W.w_dtype == KH_I8) {
+  if (W.w_dtype == KH_I8 || W.w_dtype == KH_I8P) {
     if (!W.s) return e.fail("gemm: int8 weights need scales");
     if (W.s_dtype != KH_F32 && W.s_dtype != KH_F16 && W.s_dtype != KH_BF16) return e.fail("gemm: bad scale dtype");
     if (ldw % 16) return e.fail("gemm: int8 ldw=%d must be a multiple of 16", ldw);
@@ -176,6 +176,11 @@ int gemm_run(hipStream_t st, int epi, const void* A, int a_dtype, const kh_weigh
       if (group % BK || K % group) return e.fail("gemm: int8 group %d must divide K and be a multiple of 64", group);
       if (group & (group - 1)) return e.fail("gemm: int8 group %d must be a power of two", group);
       wf = W.s_dtype == KH_F32 ? WF_I8_GROUP : W.s_dtype == KH_F16 ? WF_I8_GROUP_F16 : WF_I8_GROUP_BF16;
+    }
+    if (W.w_dtype == KH_I8P) {
+      if (wf != WF_I8_CHANNEL && wf != WF_I8_GROUP)
+        return e.fail("gemm: packed int8 weights need per-channel scales or f32 group scales");
+      wf |= WF_PK;
     }
   } else {
     if (W.w_dtype != a_dtype) return e.fail("gemm: 16-bit weights must match the activation type");
@@ -201,6 +206,41 @@ int gemm_run(hipStream_t st, int epi, const void* A, int a_dtype, const kh_weigh
 }
 
 }  // namespace
+
+// ---- kh_pack_int8: thread = one (8-row panel, 4-column group): eight 4-byte row reads, one 32-byte write ----
+__global__ __launch_bounds__(256) void pack_int8_kernel(const uint8_t* __restrict__ W, int ldw, long long groups,
+                                                       uint8_t* __restrict__ out) {
+  const long long g = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (g >= groups) return;
+  const int per_panel = ldw / 4;
+  const long long panel = g / per_panel;
+  const int cg = (int)(g - panel * per_panel);
+  const uint8_t* src = W + (size_t)panel * 8 * ldw + 4 * cg;
+  u32x4 a, b;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    a[i] = *(const uint32_t*)(src + (size_t)i * ldw);
+    b[i] = *(const uint32_t*)(src + (size_t)(i + 4) * ldw);
+  }
+  u32x4* dst = (u32x4*)(out + (size_t)panel * 8 * ldw + 32 * cg);
+  dst[0] = a;
+  dst[1] = b;
+}
+
+int pack_int8(hipStream_t st, const void* W, int K, int ldw, void* out, Err& e) {
+  if (!W || !out) return e.fail("pack_int8: null W / out");
+  if (K <= 0 || K % 8) return e.fail("pack_int8: K=%d must be a positive multiple of 8", K);
+  if (ldw <= 0 || ldw % 16) return e.fail("pack_int8: ldw=%d must be a positive multiple of 16", ldw);
+  if (((uintptr_t)W | (uintptr_t)out) & 15) return e.fail("pack_int8: W and out must be 16-byte aligned");
+  const size_t bytes = (size_t)K * ldw;
+  const uintptr_t w0 = (uintptr_t)W, o0 = (uintptr_t)out;
+  if (w0 < o0 + bytes && o0 < w0 + bytes) return e.fail("pack_int8: out overlaps W");
+  const long long groups = (long long)(K / 8) * (ldw / 4);
+  hipLaunchKernelGGL(pack_int8_kernel, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, st, (const uint8_t*)W, ldw,
+                     groups, (uint8_t*)out);
+  const hipError_t r = hipGetLastError();
+  return r == hipSuccess ? KH_OK : e.hip(r, "pack_int8 launch");
+}
 
 int gemm(hipStream_t st, int epi, const void* A, int a_dtype, const kh_weight& W, void* C, int M, int N, int K,
          int lda, int ldw, int ldc, const void* vec, Err& e) {

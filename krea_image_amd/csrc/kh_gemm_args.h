@@ -17,6 +17,9 @@ constexpr int GROUP_M = 4;  // tile rows per group (measured: 4 edges out 2, 8 a
 
 // weight formats; the group formats carry their scale type in the kernel so the K loop has no branches
 enum { WF_16 = 0, WF_I8_CHANNEL = 1, WF_I8_GROUP = 2, WF_I8_GROUP_F16 = 3, WF_I8_GROUP_BF16 = 4 };
+// flag on an int8 format: the weights are in the packed layout of kh_pack_int8 (each thread's 8 k-rows x 4
+// columns contiguous, read with two 16-byte loads instead of eight 4-byte ones)
+constexpr int WF_PK = 8;
 // internal epilogue: STORE16 followed by the per-head RMSNorm + RoPE of the q and k heads (qk_norm_rope fused;
 // GemmArgs qk_*). Needs 256-wide tiles: each wave's 128 columns are then one head.
 constexpr int EPI_QKNR = 8;

@@ -73,7 +73,10 @@ __device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, const f
 // bits for the group format: f32, or f16 / bf16 in the low half).
 template <int WF, int KR>
 struct WRaw {
-  uint32_t r[KR];
+  union {
+    uint32_t r[KR];
+    u32x4 v[KR / 4];  // the packed layout's 16-byte loads
+  };
   uint32_t s[4];
 };
 template <int KR>
@@ -153,8 +156,12 @@ struct Cfg {
 // channels, and fill a wave of workgroups where 256 would leave CUs idle, e.g. 4096 x 3072 outputs: 16 x 16
 // tiles of 192 instead of 16 x 12). The waves' n extent is TN / 2 = JB blocks of 32.
 // CONV: the activation tile is gathered from an image as an implicit 3 x 3 convolution (GemmArgs cv_*).
-template <int ACT, int WF, int EPI, int WAVES, bool SK, int TN = BN, bool CONV = false>
+// WFX: weight format, optionally | WF_PK (packed int8 layout).
+template <int ACT, int WFX, int EPI, int WAVES, bool SK, int TN = BN, bool CONV = false>
 __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
+  constexpr bool PK = (WFX & WF_PK) != 0;
+  constexpr int WF = WFX & ~WF_PK;
+  static_assert(!PK || (WF != WF_16 && !CONV), "packed layout: int8 weights, plain GEMM");
   using C_ = Cfg<WAVES>;
   static_assert(TN == BN || ((TN == 192 || TN == 128) && !SK && !wide_only(EPI)),
                 "narrow tiles (192 / 128): data-parallel, no SwiGLU");
@@ -260,11 +267,19 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
       }
     }
     wcol = min(n0 + wl * 4, p.N - 4);
-    wbase = (const char*)p.W + ((size_t)(wave * KR) * p.ldw + wcol) * WB;
+    // packed: 8-row panels of 8 ldw bytes, column group c / 4 at 32 (c / 4) = 8 c within the panel
+    wbase = (const char*)p.W + ((size_t)(wave * KR) * p.ldw + (PK ? 8 : 1) * wcol) * WB;
   };
   // untracked loads (see vm_load_b32): their waits are the explicit vmcnt of step() / the prologue
   auto issue_w = [&](int t, WRaw<WF, KR>& R) {
     const char* src = wbase + (size_t)((kb + t) * BK) * wrow;
+    if constexpr (PK) {
+#pragma unroll
+      for (int i = 0; i < KR / 8; i++) {  // panel i: rows 8 i .. 8 i + 7 of this thread, 32 contiguous bytes
+        R.v[2 * i] = vm_load_b128(src + (size_t)i * 8 * wrow);
+        R.v[2 * i + 1] = vm_load_b128(src + (size_t)i * 8 * wrow + 16);
+      }
+    } else
 #pragma unroll
     for (int i = 0; i < KR; i++) {
       if constexpr (WF == WF_16)
@@ -287,8 +302,13 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
   auto ready_w = [&](WRaw<WF, KR>& R, auto newer_c) {
     constexpr int NEWER = decltype(newer_c)::value;
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NEWER));
+    if constexpr (PK) {
 #pragma unroll
-    for (int i = 0; i < KR; i++) vm_ready(R.r[i]);
+      for (int i = 0; i < KR / 4; i++) vm_ready(R.v[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < KR; i++) vm_ready(R.r[i]);
+    }
     if constexpr (is_group(WF)) {
 #pragma unroll
       for (int j = 0; j < 4; j++) vm_ready(R.s[j]);
@@ -328,7 +348,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
   };
 
   int ns = 0;  // K steps of the current segment
-  constexpr int LOADS = C_::LOADS + (is_group(WF) ? 4 : 0);
+  constexpr int LOADS = (PK ? X_LOADS + KR / 4 : C_::LOADS) + (is_group(WF) ? 4 : 0);
   using NewerT = std::integral_constant<int, LOADS>;
 
   // One K step: multiply stage t; convert raw(t + 1) into the other W stage between the MFMAs; the loads
@@ -714,6 +734,8 @@ template <int ACT>
 hipError_t launch_wf(int wf, int epi, const GemmArgs& a, int g, int tn, hipStream_t st) {
   if (wf == WF_16) return launch_epi<ACT, WF_16>(epi, a, g, tn, st);
   if (wf == WF_I8_CHANNEL) return launch_epi<ACT, WF_I8_CHANNEL>(epi, a, g, tn, st);
+  if (wf == (WF_I8_CHANNEL | WF_PK)) return launch_epi<ACT, WF_I8_CHANNEL | WF_PK>(epi, a, g, tn, st);
+  if (wf == (WF_I8_GROUP | WF_PK)) return launch_epi<ACT, WF_I8_GROUP | WF_PK>(epi, a, g, tn, st);
   if (wf == WF_I8_GROUP) return launch_epi<ACT, WF_I8_GROUP>(epi, a, g, tn, st);
   if (wf == WF_I8_GROUP_F16) return launch_epi<ACT, WF_I8_GROUP_F16>(epi, a, g, tn, st);
   return launch_epi<ACT, WF_I8_GROUP_BF16>(epi, a, g, tn, st);

@@ -32,6 +32,7 @@ struct Err {
   }
 };
 
+int pack_int8(hipStream_t st, const void* W, int K, int ldw, void* out, Err& e);
 int gemm(hipStream_t st, int epi, const void* A, int a_dtype, const kh_weight& W, void* C, int M, int N, int K,
          int lda, int ldw, int ldc, const void* vec, Err& e);
 // the per-head RMSNorm + RoPE of qk_norm_rope fused into a STORE16 GEMM's epilogue

@@ -425,7 +425,8 @@ int gemv(hipStream_t st, const float* x, const kh_weight& W, float* y, int rows,
   } else if (W.w_dtype == KH_F16 || W.w_dtype == KH_BF16) {
     wf = 0;
   } else {
-    return e.fail("gemv: weight dtype must be int8, f16 or bf16");
+    return e.fail(W.w_dtype == KH_I8P ? "gemv: packed int8 weights (KH_I8P) are for kh_gemm; pass the KH_I8 layout"
+                                      : "gemv: weight dtype must be int8, f16 or bf16");
   }
   // K split so the grid has >= wg_target workgroups; each slab's x fits the 512-entry LDS stage
   const int cols = wf == 0 ? 128 : 256;

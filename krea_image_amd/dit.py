@@ -112,13 +112,14 @@ def random_layer(shape: DitShape, gen: torch.Generator, dev) -> DitLayerWeights:
         from .qw import RawWeight
         none = RawWeight(0, None, kh.I8, kh.F32, 0)
         return DitLayerWeights(
-            qkv=lin(D, shape.qkv_cols), o=lin(D, D), up=lin(D, shape.up_cols), down=lin(shape.ff, D), ada=none,
+            qkv=lin(D, shape.qkv_cols).pack(), o=lin(D, D).pack(), up=lin(D, shape.up_cols).pack(),
+            down=lin(shape.ff, D).pack(), ada=none,
             ada_bias=None, n1=norm_w(D), n2=norm_w(D), qn=norm_w(128), kn=norm_w(128),
             mod_table=0.1 * torch.randn(6 * D, generator=gen, device=dev))
 
     return DitLayerWeights(
-        qkv=_int8_weight(D, shape.qkv_cols, gen, dev), o=_int8_weight(D, D, gen, dev),
-        up=_int8_weight(D, shape.up_cols, gen, dev), down=_int8_weight(shape.ff, D, gen, dev),
+        qkv=_int8_weight(D, shape.qkv_cols, gen, dev).pack(), o=_int8_weight(D, D, gen, dev).pack(),
+        up=_int8_weight(D, shape.up_cols, gen, dev).pack(), down=_int8_weight(shape.ff, D, gen, dev).pack(),
         ada=_int8_weight(cd, 6 * D, gen, dev), ada_bias=0.01 * torch.randn(6 * D, generator=gen, device=dev),
         n1=norm_w(D), n2=norm_w(D), qn=norm_w(128), kn=norm_w(128))
 

@@ -18,7 +18,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libkh.so")
 
-F32, F16, BF16, I8 = 0, 1, 2, 3
+F32, F16, BF16, I8, I8P = 0, 1, 2, 3, 4  # I8P: int8 in the packed layout of pack_int8
 EPI = {"store16": 0, "f32": 1, "resid_gate": 2, "resid": 3, "swiglu": 4, "gelu": 5, "bias16": 6, "bias_f32": 7}
 # reference spelling (enum class Epi, engine/src/metal.h:37-38)
 Epi = type("Epi", (), {"BF16": 0, "STORE16": 0, "F32": 1, "ResidGate": 2, "Resid": 3, "SwiGLU": 4, "GELU": 5,
@@ -32,7 +32,8 @@ SYMBOLS = ["kh_version", "kh_gemm", "kh_attention", "kh_rms_norm", "kh_qk_norm_r
            "kh_qw_open", "kh_qw_close", "kh_qw_count", "kh_qw_version", "kh_qw_meta", "kh_qw_at", "kh_qw_find",
            "kh_qw_upload", "kh_stream_create", "kh_stream_destroy", "kh_stream_sync", "kh_alloc", "kh_free",
            "kh_upload", "kh_download", "kh_vae_conv3x3", "kh_vae_subpix_weights", "kh_vae_conv_up2", "kh_vae_im2col", "kh_vae_norm_silu", "kh_vae_unpack", "kh_vae_softmax",
-           "kh_vae_conv_out", "kh_vae_workspace_bytes", "kh_vae_decode", "kh_gemm_qk_norm_rope"]
+           "kh_vae_conv_out", "kh_vae_workspace_bytes", "kh_vae_decode", "kh_gemm_qk_norm_rope",
+           "kh_pack_int8"]
 
 
 class KhError(RuntimeError):
@@ -93,6 +94,7 @@ def load():
         lib.kh_gemm_qk_norm_rope.argtypes = ([vp, vp, i, ctypes.POINTER(_WeightC), vp] + [i] * 6 + [vp] * 4 +
                                              [i] * 4 + [ctypes.c_float, i, i, vp, vp, cp, i])
         lib.kh_gemm_qk_norm_rope.restype = i
+        lib.kh_pack_int8.argtypes, lib.kh_pack_int8.restype = [vp, vp, i, i, vp, cp, i], i
         lib.kh_rope_tables.argtypes = [i, i, i, i, vp, vp]
         lib.kh_dit_layer_forward.argtypes = [vp, ctypes.POINTER(DitConfig), ctypes.POINTER(DitLayerC),
                                              ctypes.POINTER(DitStateC), i, cp, i]
@@ -132,18 +134,36 @@ def _check(rc, err):
 @dataclass
 class Weight:
     """Input-major GEMM weight Wt[K, N] (engine/src/metal.h:25-29). w: int8 / fp16 / bf16 device tensor;
-    s: scales — [K/group, N] for group < K, [N] for per-output-channel (group = K or 0)."""
+    s: scales — [K/group, N] for group < K, [N] for per-output-channel (group = K or 0).
+    packed: w holds int8 in the layout of pack_int8 (kh_gemm reads it as KH_I8P; same results bitwise)."""
     w: torch.Tensor
     s: Optional[torch.Tensor] = None
     group: int = 0
+    packed: bool = False
 
     @property
     def q8(self) -> bool:
         return self.w.dtype == torch.int8
 
     def c(self) -> _WeightC:
-        return _WeightC(self.w.data_ptr(), 0 if self.s is None else self.s.data_ptr(), dtype_code(self.w.dtype),
+        return _WeightC(self.w.data_ptr(), 0 if self.s is None else self.s.data_ptr(),
+                        I8P if self.packed else dtype_code(self.w.dtype),
                         F32 if self.s is None else dtype_code(self.s.dtype), self.group)
+
+    def pack(self) -> "Weight":
+        """The same weight in kh_gemm's packed int8 layout (a new device buffer; scales shared)."""
+        if self.packed:
+            return self
+        return Weight(pack_int8(self.w), self.s, self.group, True)
+
+
+def pack_int8(w: torch.Tensor) -> torch.Tensor:
+    """kh_pack_int8: int8 Wt[K, ldw] (contiguous) -> the packed layout, a new tensor of the same shape."""
+    if w.dtype != torch.int8 or w.dim() != 2 or not w.is_contiguous():
+        raise KhError("pack_int8: expects a contiguous 2-D int8 tensor")
+    out = torch.empty_like(w)
+    _call(load().kh_pack_int8, _stream(), _ptr(w), w.shape[0], w.shape[1], _ptr(out))
+    return out
 
 
 _F32_OUT_EPI = (1, 2, 3, 7)  # F32, RESID_GATE, RESID, BIAS_F32
@@ -177,7 +197,11 @@ def gemm(epi, A: torch.Tensor, W: Weight, C: torch.Tensor, M: int, N: int, K: in
             raise KhError(f"gemm: epilogue {epi} writes {want}, C is {C.dtype}")
         _need(A, "A", M, K, lda, A.element_size())
         _need(C, "C", M, N // 2 if epi == EPI["swiglu"] else N, ldc, C.element_size())
-        _need(W.w, "W", K, N, ldw, 1 if W.w.dtype == torch.int8 else 2)
+        if W.packed:  # 8-row panels of 8 ldw bytes; columns [0, N) end at byte 8 N of the last panel
+            if _bytes_after(W.w) < (K - 8) * ldw + 8 * N:
+                raise KhError(f"gemm: W holds {_bytes_after(W.w)} bytes, the call addresses {(K - 8) * ldw + 8 * N}")
+        else:
+            _need(W.w, "W", K, N, ldw, 1 if W.w.dtype == torch.int8 else 2)
         if vec is not None:
             _need(vec, "vec", 1, N, N, 4)
     err = ctypes.create_string_buffer(512)

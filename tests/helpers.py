@@ -61,3 +61,15 @@ def weight_to_dev(wd, dev):
         else:
             s = to_dev16(wd["s"], wd["s_dtype"], dev)
     return kh.Weight(w, s, wd["group"])
+
+
+def unpack_int8(packed):
+    """Inverse of kh_pack_int8's layout (byte (k // 8) 8 ldw + 32 (n // 4) + 4 (k % 8) + n % 4 holds (k, n))."""
+    K, L = packed.shape
+    return np.ascontiguousarray(packed.reshape(K // 8, L // 4, 8, 4).transpose(0, 2, 1, 3).reshape(K, L))
+
+
+def host_int8(W):
+    """The input-major int8 matrix of a kh.Weight, packed or not, as numpy."""
+    q = W.w.cpu().numpy()
+    return unpack_int8(q) if getattr(W, "packed", False) else q

@@ -7,7 +7,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
-from tests.helpers import from_dev16, rel_l2
+from tests.helpers import from_dev16, host_int8, rel_l2
 
 pytestmark = pytest.mark.gpu
 TOL = 1.6e-2
@@ -27,7 +27,7 @@ def np16(t):
 def oracle_layer(shape, L, x, cond, cos, sin):
     dt = O.F16 if shape.dtype == torch.float16 else O.BF16
     D, kvD = shape.dim, shape.kv_heads * 128
-    w = lambda W: (W.w.cpu().numpy(), O.I8, np16(W.s), O.F16, W.w.shape[0])  # noqa: E731
+    w = lambda W: (host_int8(W), O.I8, np16(W.s), O.F16, W.w.shape[0])  # noqa: E731
     tvec = O.gemv(cond[None].astype(np.float32), *w(L.ada), act=1, bias=L.ada_bias.cpu().numpy())[0]
     mods = O.make_cond(tvec, None, L.n1.cpu().numpy(), L.n2.cpu().numpy())
     h = O.rms_norm(x, mods[0], mods[1], dt, shape.eps, shape.norm_center)
