@@ -148,6 +148,22 @@ int kh_gemm_f32(kh_stream stream, const float* A, const float* W, float* C, int 
  * mode 1: 2-D, theta 10000, pairs [0, 32) by row and [32, 64) by column (benchmark configs). */
 int kh_rope_tables(int T, int H, int W, int mode, float* cosb, float* sinb);
 
+/* ---- the sampler around the DiT forward (engine/src/pipeline.mm:300-316) ---- */
+
+/* Flow-matching noise levels on the HOST: out[i] = e / (e + (1/t - 1)), e = exp(mu), t = 1 - i / steps, for
+ * i = 0 .. steps (out holds steps + 1 floats; out[steps] = 0), computed in double, stored as float.
+ * Replaces krea_sigmas (engine/src/model.mm:594-602; the reference's default mu is 1.15, model.h:215). */
+int kh_sigmas(int steps, float mu, float* out);
+
+/* Euler step of the latent, z[i] += dt v[i] (f32, n elements, one fused multiply-add per element), dt =
+ * sigma[i + 1] - sigma[i]. Replaces Metal::euler_step (engine/src/metal.mm:232-235, norm.metal:234-238). */
+int kh_euler_step(kh_stream stream, float* z, const float* v, long long n, float dt, char* err, int errlen);
+
+/* Classifier-free guidance, vc[i] = vc[i] + scale (vc[i] - vn[i]) (f32, n elements, the difference then one
+ * fused multiply-add). Replaces the cfg_combine kernel (engine/kernels/norm.metal:259-262,
+ * engine/src/pipeline.mm:311-314). */
+int kh_cfg_combine(kh_stream stream, float* vc, const float* vn, long long n, float scale, char* err, int errlen);
+
 /* ---- one DiT block on the device: engine/src/model.mm:369-385 (DiT::layer) ---- */
 typedef struct kh_dit_config {
   int dim;         /* hidden size D */

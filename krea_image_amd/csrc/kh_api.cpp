@@ -81,6 +81,20 @@ int kh_rope_tables(int T, int H, int W, int mode, float* cosb, float* sinb) {
   return kh::rope_tables(T, H, W, mode, cosb, sinb);
 }
 
+int kh_sigmas(int steps, float mu, float* out) { return kh::sigmas(steps, mu, out); }
+
+int kh_euler_step(kh_stream stream, float* z, const float* v, long long n, float dt, char* err, int errlen) {
+  kh::Err e{err, errlen};
+  e.clear();
+  return kh::euler_step((hipStream_t)stream, z, v, n, dt, e);
+}
+
+int kh_cfg_combine(kh_stream stream, float* vc, const float* vn, long long n, float scale, char* err, int errlen) {
+  kh::Err e{err, errlen};
+  e.clear();
+  return kh::cfg_combine((hipStream_t)stream, vc, vn, n, scale, e);
+}
+
 int kh_dit_layer_forward(kh_stream stream, const kh_dit_config* cfg, const kh_dit_layer* layer,
                          const kh_dit_state* state, int rows, char* err, int errlen) {
   kh::Err e{err, errlen};

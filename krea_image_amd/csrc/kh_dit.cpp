@@ -81,6 +81,17 @@ int dit_forward(hipStream_t st, const kh_dit_config& c, const kh_dit_layer* laye
 }
 
 // engine/src/model.mm:290-315 (mode 0) and the 2-D variant of the benchmark configs (mode 1)
+// krea_sigmas (engine/src/model.mm:594-602)
+int sigmas(int steps, float mu, float* out) {
+  if (steps <= 0 || !out) return KH_EINVAL;
+  const double e = std::exp((double)mu);
+  for (int i = 0; i <= steps; i++) {
+    const double t = 1.0 - (double)i / steps;
+    out[i] = t <= 0 ? 0.0f : (float)(e / (e + (1.0 / t - 1.0)));
+  }
+  return KH_OK;
+}
+
 int rope_tables(int T, int H, int W, int mode, float* cosb, float* sinb) {
   if (T < 0 || H < 0 || W < 0 || (mode != 0 && mode != 1) || !cosb || !sinb) return KH_EINVAL;
   double om[64];

@@ -71,6 +71,9 @@ int dit_layer_forward(hipStream_t st, const kh_dit_config& c, const kh_dit_layer
 int dit_forward(hipStream_t st, const kh_dit_config& c, const kh_dit_layer* layers, int n, const kh_dit_state& s,
                 int R, Err& e);
 int rope_tables(int T, int H, int W, int mode, float* cosb, float* sinb);
+int sigmas(int steps, float mu, float* out);
+int euler_step(hipStream_t st, float* z, const float* v, long long n, float dt, Err& e);
+int cfg_combine(hipStream_t st, float* vc, const float* vn, long long n, float scale, Err& e);
 
 int vae_unpack(hipStream_t st, const float* z, const float* mean, const float* stdv, const float* w, const float* b,
                void* y, int H16, int W16, Err& e);

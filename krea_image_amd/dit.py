@@ -187,6 +187,19 @@ class DitRunner:
         kh.gemm_f32(self.hf, self.last_w, vel, M, C, D, D, C, C, 1, self.last_b)
         return vel
 
+    def denoise(self, txt: torch.Tensor, z: torch.Tensor, sig, vel: Optional[torch.Tensor] = None,
+                before_step=None):
+        """The denoising loop of engine/src/pipeline.mm:300-316 without guidance or masks: for each step i,
+        velocity = forward(txt, z), then z += (sig[i + 1] - sig[i]) velocity (kh_euler_step), in place on z.
+        before_step(i), if given, runs first in each step (e.g. QwDit.set_cond for the step's noise level)."""
+        vel = torch.empty_like(z) if vel is None else vel
+        for i in range(len(sig) - 1):
+            if before_step is not None:
+                before_step(i)
+            self.forward(txt, z, vel)
+            kh.euler_step(z, vel, float(sig[i + 1]) - float(sig[i]))
+        return z
+
 
 # ---------------------------------------------------------------------------------------------------------
 # a DiT from a packed .qw file (the reference architecture)

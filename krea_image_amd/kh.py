@@ -33,7 +33,7 @@ SYMBOLS = ["kh_version", "kh_gemm", "kh_attention", "kh_rms_norm", "kh_qk_norm_r
            "kh_qw_upload", "kh_stream_create", "kh_stream_destroy", "kh_stream_sync", "kh_alloc", "kh_free",
            "kh_upload", "kh_download", "kh_vae_conv3x3", "kh_vae_subpix_weights", "kh_vae_conv_up2", "kh_vae_im2col", "kh_vae_norm_silu", "kh_vae_unpack", "kh_vae_softmax",
            "kh_vae_conv_out", "kh_vae_workspace_bytes", "kh_vae_decode", "kh_gemm_qk_norm_rope",
-           "kh_pack_int8"]
+           "kh_pack_int8", "kh_sigmas", "kh_euler_step", "kh_cfg_combine"]
 
 
 class KhError(RuntimeError):
@@ -95,6 +95,10 @@ def load():
                                              [i] * 4 + [ctypes.c_float, i, i, vp, vp, cp, i])
         lib.kh_gemm_qk_norm_rope.restype = i
         lib.kh_pack_int8.argtypes, lib.kh_pack_int8.restype = [vp, vp, i, i, vp, cp, i], i
+        lib.kh_sigmas.argtypes, lib.kh_sigmas.restype = [i, ctypes.c_float, vp], i
+        ll = ctypes.c_longlong
+        lib.kh_euler_step.argtypes, lib.kh_euler_step.restype = [vp, vp, vp, ll, ctypes.c_float, cp, i], i
+        lib.kh_cfg_combine.argtypes, lib.kh_cfg_combine.restype = [vp, vp, vp, ll, ctypes.c_float, cp, i], i
         lib.kh_rope_tables.argtypes = [i, i, i, i, vp, vp]
         lib.kh_dit_layer_forward.argtypes = [vp, ctypes.POINTER(DitConfig), ctypes.POINTER(DitLayerC),
                                              ctypes.POINTER(DitStateC), i, cp, i]
@@ -306,3 +310,36 @@ def rope_tables(T: int, H: int, W: int, mode: int):
     if load().kh_rope_tables(T, H, W, mode, ctypes.c_void_p(c.data_ptr()), ctypes.c_void_p(s.data_ptr())) != 0:
         raise KhError("rope_tables: bad arguments")
     return c, s
+
+
+def sigmas(steps: int, mu: float = 1.15):
+    """krea_sigmas (engine/src/model.mm:594-602), on the host: numpy f32 [steps + 1], 1 -> 0."""
+    import numpy as np
+    out = np.empty(steps + 1, np.float32)
+    if load().kh_sigmas(steps, mu, out.ctypes.data) != 0:
+        raise KhError(f"sigmas: steps={steps} must be positive")
+    return out
+
+
+def _f32_flat(t, name):
+    if t.dtype != torch.float32 or not t.is_contiguous():
+        raise KhError(f"{name}: expects a contiguous float32 tensor")
+    return t.numel()
+
+
+def euler_step(z: torch.Tensor, v: torch.Tensor, dt: float):
+    """Metal::euler_step (engine/src/metal.mm:232-235): z += dt v in place (f32)."""
+    n = _f32_flat(z, "euler_step")
+    if _f32_flat(v, "euler_step") != n:
+        raise KhError("euler_step: z and v differ in size")
+    _call(load().kh_euler_step, _stream(), _ptr(z), _ptr(v), n, dt)
+    return z
+
+
+def cfg_combine(vc: torch.Tensor, vn: torch.Tensor, scale: float):
+    """cfg_combine (engine/kernels/norm.metal:259-262): vc += scale (vc - vn) in place (f32)."""
+    n = _f32_flat(vc, "cfg_combine")
+    if _f32_flat(vn, "cfg_combine") != n:
+        raise KhError("cfg_combine: vc and vn differ in size")
+    _call(load().kh_cfg_combine, _stream(), _ptr(vc), _ptr(vn), n, scale)
+    return vc

@@ -20,6 +20,10 @@
  *   or_rope_tables          closed form of model.mm:295-315 evaluated at chosen (i, j) positions.
  *   or_attention            torch scaled_dot_product_attention in fp64 (non-causal, causal, GQA); uniform-V
  *                           and one-hot-key invariants; sigmoid gate elementwise.
+ *   or_sigmas               closed forms: mu = 0 gives the linear schedule t = 1 - i / steps; endpoints 1 and
+ *                           0; strictly decreasing; the logistic identity log(s / (1 - s)) = mu + log(t / (1 - t)).
+ *   or_euler_step,          numpy float64 of the update rounded once to f32 (exactly the single rounding of an
+ *   or_cfg_combine          fma); dt = 0 / scale = 0 leave the input unchanged.
  */
 #include "oracle.h"
 
@@ -618,4 +622,24 @@ void or_vae_conv_out(const uint16_t* x, int C, const uint16_t* w, const float* b
       rgba[(size_t)pix * 4 + k] = (uint8_t)a;
     }
   }
+}
+
+/* ---------------------------------------------------------------------------------------------- */
+/* Sampler: engine/src/model.mm:594-602 (krea_sigmas), engine/kernels/norm.metal:234-238 (euler_step) and
+ * 259-262 (cfg_combine).                                                                          */
+
+void or_sigmas(int steps, float mu, float* out) {
+  const double e = exp((double)mu);
+  for (int i = 0; i <= steps; i++) {
+    const double t = 1.0 - (double)i / steps;
+    out[i] = t <= 0 ? 0.0f : (float)(e / (e + (1.0 / t - 1.0)));
+  }
+}
+
+void or_euler_step(float* z, const float* v, long long n, float dt) {
+  for (long long i = 0; i < n; i++) z[i] = fmaf(dt, v[i], z[i]);
+}
+
+void or_cfg_combine(float* vc, const float* vn, long long n, float scale) {
+  for (long long i = 0; i < n; i++) vc[i] = fmaf(scale, vc[i] - vn[i], vc[i]);
 }

@@ -72,6 +72,14 @@ void or_qk_norm_rope(void* qkv, int dtype, const float* wq, const float* wk, con
  *         omega_p = theta^(-2 (p mod 32) / 64). */
 void or_rope_tables(int T, int H, int W, int mode, float* cosb, float* sinb);
 
+/* The sampler around the DiT forward (engine/src/pipeline.mm:300-316):
+ * or_sigmas: krea_sigmas (engine/src/model.mm:594-602), steps + 1 floats;
+ * or_euler_step: z += dt v (engine/kernels/norm.metal:234-238), one fused multiply-add per element;
+ * or_cfg_combine: vc = vc + scale (vc - vn) (engine/kernels/norm.metal:259-262), difference then one fma. */
+void or_sigmas(int steps, float mu, float* out);
+void or_euler_step(float* z, const float* v, long long n, float dt);
+void or_cfg_combine(float* vc, const float* vn, long long n, float scale);
+
 /* engine/kernels/attention.metal:131-351 (attention_d128) + engine/src/metal.mm:193-202:
  * O = softmax(Q K^T / sqrt(128) (+ QB KB^T)) V (* sigmoid(G)), head dim 128, GQA group, optional causal
  * mask (key j visible to query i iff j <= i + q_pos0). Scores / softmax in fp32, P rounded to the 16-bit

@@ -206,6 +206,25 @@ def qk_norm_rope(qkv, dtype, wq, wk, cosb, sinb, q_off, n_q, k_off, n_k, eps=1e-
     return qkv, qbig, kbig
 
 
+def sigmas(steps, mu=1.15):
+    out = np.empty(steps + 1, np.float32)
+    lib().or_sigmas(steps, ctypes.c_float(mu), _p(out))
+    return out
+
+
+def euler_step(z, v, dt):
+    z = np.array(z, np.float32, copy=True)
+    lib().or_euler_step(_p(z), _p(np.ascontiguousarray(v, np.float32)), ctypes.c_longlong(z.size), ctypes.c_float(dt))
+    return z
+
+
+def cfg_combine(vc, vn, scale):
+    vc = np.array(vc, np.float32, copy=True)
+    lib().or_cfg_combine(_p(vc), _p(np.ascontiguousarray(vn, np.float32)), ctypes.c_longlong(vc.size),
+                         ctypes.c_float(scale))
+    return vc
+
+
 def rope_tables(T, H, W, mode):
     R = T + H * W
     c = np.empty((R, 64), np.float32)
