@@ -153,6 +153,10 @@ int gemm_run(hipStream_t st, int epi, const void* A, int a_dtype, const kh_weigh
   if (!A || !W.w || !C) return e.fail("gemm: null A / W / C");
   if (lda < K || lda % 8) return e.fail("gemm: lda=%d must be >= K and a multiple of 8", lda);
   if (ldw < N) return e.fail("gemm: ldw=%d < N=%d", ldw, N);
+  // the activation loader indexes A with 32-bit element offsets (row * lda + k)
+  if ((long long)(M - 1) * lda + K >= (1LL << 31))
+    return e.fail("gemm: A spans (M - 1) * lda + K = %lld elements, more than 2^31 - 1: split the rows",
+                  (long long)(M - 1) * lda + K);
   const int out_cols = epi == KH_EPI_SWIGLU ? N / 2 : N;
   const bool out16 = epi == KH_EPI_STORE16 || epi == KH_EPI_GELU || epi == KH_EPI_BIAS16 || epi == KH_EPI_SWIGLU;
   const int ldc_mult = out16 ? 8 : 4;  // output rows are written in 16-byte vectors

@@ -69,6 +69,7 @@ def _gemm_call(lib, **kw):
     (dict(epi=2), "needs vec"),
     (dict(w=None), "null weight"),
     (dict(A=0), "null"),
+    (dict(M=1 << 20, lda=4096), "2^31"),
 ])
 def test_gemm_rejects_without_launch(lib, kw, msg):
     rc, err = _gemm_call(lib, **kw)
