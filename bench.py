@@ -24,7 +24,7 @@ Reported beside it:
                  heads, [3] one DiT block at 4608 rows, [4] the full step swept over 1024 / 4096 / 8192
                  image tokens + 512 text tokens; and the VAE decode of a 64 x 64 latent to 1024^2 RGBA.
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-dit] [--probe {gemm,attention,dit,vae}]
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-dit] [--probe {gemm,attention,dit,dit_ref,vae}]
 """
 import argparse
 import json
@@ -188,11 +188,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-dit", action="store_true", help="skip the full DiT step latency")
-    ap.add_argument("--probe", nargs="?", const="gemm", choices=["gemm", "attention", "dit", "vae"],
+    ap.add_argument("--probe", nargs="?", const="gemm", choices=["gemm", "attention", "dit", "dit_ref", "vae"],
                     help="profiling probe, no JSON line: 'gemm' = one up-projection launch and one 512 MiB device "
                          "copy (for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE calibration); 'attention' = three "
                          "launches of the joint attention of config [2] (4608 tokens x 24 heads, fp16); 'dit' = two full "
-                         "DiT steps at 1024^2 (71 blocks); 'vae' = the VAE decode of a 64 x 64 "
+                         "DiT steps at 1024^2 (71 blocks); 'dit_ref' = two reference-architecture steps (28 blocks); "
+                         "'vae' = the VAE decode of a 64 x 64 "
                          "latent (1024^2 RGBA), 2 + 5 calls")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -223,6 +224,10 @@ def main():
     if args.probe == "dit":
         from krea_image_amd import dit
         dit.bench_step(dev, rows_img=4096, rows_txt=512, layers=71, steps=2)
+        return
+    if args.probe == "dit_ref":
+        from krea_image_amd import dit
+        dit.bench_step(dev, rows_img=4096, rows_txt=512, shape=dit.reference_shape(28), steps=2)
         return
     if args.probe == "vae":
         print(json.dumps(vae_decode_bench(dev)), flush=True)
