@@ -256,6 +256,7 @@ int kh_alloc(void** out, size_t bytes, char* err, int errlen);/* hipMalloc; Meta
 int kh_free(void* p);
 int kh_upload(kh_stream s, void* dst, const void* src, size_t bytes, char* err, int errlen);   /* H2D, synchronous */
 int kh_download(kh_stream s, void* dst, const void* src, size_t bytes, char* err, int errlen); /* D2H, synchronous */
+int kh_copy(kh_stream s, void* dst, const void* src, size_t bytes, char* err, int errlen);     /* D2D, stream-ordered */
 
 /* ---- VAE decoder (Qwen-Image / Wan 2.1 VAE, single frame), NHWC bf16 activations [pixel, channel] ----
  * The convolutions run on the GEMM core against the converter's Wt[(ky*3+kx)*Cin + ci, co] 16-bit weights

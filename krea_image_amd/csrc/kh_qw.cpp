@@ -530,4 +530,14 @@ int kh_download(kh_stream s, void* dst, const void* src, size_t bytes, char* err
   return r == hipSuccess ? KH_OK : e.hip(r, "download");
 }
 
+int kh_copy(kh_stream s, void* dst, const void* src, size_t bytes, char* err, int errlen) {
+  kh::Err e{err, errlen};
+  e.clear();
+  if (bytes && (!dst || !src)) return e.fail("copy: null pointer");
+  const uintptr_t d = (uintptr_t)dst, a = (uintptr_t)src;
+  if (bytes && d < a + bytes && a < d + bytes && d != a) return e.fail("copy: overlapping ranges");
+  const hipError_t r = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, (hipStream_t)s);
+  return r == hipSuccess ? KH_OK : e.hip(r, "copy");
+}
+
 }  // extern "C"

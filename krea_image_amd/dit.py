@@ -228,16 +228,17 @@ def big_dims(f, layers: int, gain: float = 256.0) -> List[int]:
     return out
 
 
-def layers_from_qw(f, shape: DitShape, gain: float = 256.0) -> List[DitLayerWeights]:
-    """kh_dit_layer views of an uploaded file: weights stay where the upload put them (no repacking)."""
+def layers_from_qw(f, shape: DitShape, gain: float = 256.0, pack: bool = True) -> List[DitLayerWeights]:
+    """kh_dit_layer views of an uploaded file: weights stay where the upload put them; with pack=True the four
+    int8 projection weights of each layer are rearranged in place into the packed layout (QwFile.weight)."""
     from .qw import RawWeight
     none = RawWeight(0, None, kh.I8, kh.F32, 0)
     big = big_dims(f, shape.layers, gain)
     out = []
     for i in range(shape.layers):
         p = f"L{i}."
-        out.append(DitLayerWeights(qkv=f.weight(p + "qkvg"), o=f.weight(p + "o"), up=f.weight(p + "gu"),
-                                   down=f.weight(p + "down"), ada=none, ada_bias=None, n1=f.dev(p + "n1"),
+        out.append(DitLayerWeights(qkv=f.weight(p + "qkvg", pack), o=f.weight(p + "o", pack),
+                                   up=f.weight(p + "gu", pack), down=f.weight(p + "down", pack), ada=none, ada_bias=None, n1=f.dev(p + "n1"),
                                    n2=f.dev(p + "n2"), qn=f.dev(p + "qn"), kn=f.dev(p + "kn"),
                                    mod_table=f.dev(p + "mod"), big_dim=big[i]))
     return out
@@ -248,11 +249,12 @@ class QwDit(DitRunner):
     shared tvec and the file's L{i}.mod tables (on the GPU, kh_make_cond inside the layer loop), final norm
     vectors from t and last.mod (DiT::make_cond, model.mm:340-346)."""
 
-    def __init__(self, f, T: int, H: int, W: int, dev, layers: Optional[int] = None, gain: float = 256.0):
+    def __init__(self, f, T: int, H: int, W: int, dev, layers: Optional[int] = None, gain: float = 256.0,
+                 pack: bool = True):
         shape = shape_from_qw(f)
         if layers is not None:
             shape.layers = min(layers, shape.layers)
-        super().__init__(shape, T, H, W, dev, layers=layers_from_qw(f, shape, gain))
+        super().__init__(shape, T, H, W, dev, layers=layers_from_qw(f, shape, gain, pack))
         self.f = f
         self.first_w, self.first_b = f.dev("first.w"), f.dev("first.b")
         self.last_w, self.last_b = f.dev("last.w"), f.dev("last.b")

@@ -33,7 +33,7 @@ SYMBOLS = ["kh_version", "kh_gemm", "kh_attention", "kh_rms_norm", "kh_qk_norm_r
            "kh_qw_upload", "kh_stream_create", "kh_stream_destroy", "kh_stream_sync", "kh_alloc", "kh_free",
            "kh_upload", "kh_download", "kh_vae_conv3x3", "kh_vae_subpix_weights", "kh_vae_conv_up2", "kh_vae_im2col", "kh_vae_norm_silu", "kh_vae_unpack", "kh_vae_softmax",
            "kh_vae_conv_out", "kh_vae_workspace_bytes", "kh_vae_decode", "kh_gemm_qk_norm_rope",
-           "kh_pack_int8", "kh_sigmas", "kh_euler_step", "kh_cfg_combine"]
+           "kh_pack_int8", "kh_sigmas", "kh_euler_step", "kh_cfg_combine", "kh_copy"]
 
 
 class KhError(RuntimeError):
@@ -114,6 +114,7 @@ def load():
         lib.kh_free.argtypes, lib.kh_free.restype = [vp], i
         lib.kh_upload.argtypes = lib.kh_download.argtypes = [vp, vp, vp, sz, cp, i]
         lib.kh_upload.restype = lib.kh_download.restype = i
+        lib.kh_copy.argtypes, lib.kh_copy.restype = [vp, vp, vp, sz, cp, i], i
         _lib = lib
     return _lib
 

@@ -344,12 +344,25 @@ class QwFile:
             raise kh.KhError(f"{self.path} is not uploaded")
         return DevPtr(ti.dev)
 
-    def weight(self, name: str) -> RawWeight:
-        """The GEMM weight `name` (+ `name.s` for int8): Metal's Weight{w, s, q8} (engine/src/metal.h:25-29)."""
+    def weight(self, name: str, pack: bool = False) -> RawWeight:
+        """The GEMM weight `name` (+ `name.s` for int8): Metal's Weight{w, s, q8} (engine/src/metal.h:25-29).
+        pack=True rearranges an int8 weight in place into kh_gemm's packed layout (kh_pack_int8 into one scratch
+        buffer, copied back: no extra resident memory) on first request; from then on the weight is always
+        returned as KH_I8P, so its bytes are never read as the input-major layout again."""
         ti = self.info(name)
         if ti.dtype == "i8":
             si = self.info(name + ".s")
             K = ti.shape[0]
             group = K // si.shape[0] if si.shape[0] else 0
-            return RawWeight(self.dev(name).p, self.dev(name + ".s").p, kh.I8, _CODE[si.dtype], group)
+            packed = self.__dict__.setdefault("_packed", set())
+            if pack and name not in packed and (group == K or si.dtype == "f32"):
+                N = ti.shape[1]
+                import torch
+                tmp = torch.empty(K * N, dtype=torch.int8, device="cuda")
+                kh._call(kh.load().kh_pack_int8, kh._stream(), self.dev(name).p, K, N, kh._ptr(tmp))
+                kh._call(kh.load().kh_copy, kh._stream(), self.dev(name).p, kh._ptr(tmp), K * N)
+                torch.cuda.current_stream().synchronize()
+                packed.add(name)
+            return RawWeight(self.dev(name).p, self.dev(name + ".s").p, kh.I8P if name in packed else kh.I8,
+                             _CODE[si.dtype], group)
         return RawWeight(self.dev(name).p, None, _CODE[ti.dtype], kh.F32, 0)

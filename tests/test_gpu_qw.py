@@ -71,6 +71,36 @@ def test_qw_dit_forward_matches_oracle(dev, tmp_path, big_gain):
         assert np.isfinite(got).all() and err <= TOL
 
 
+def test_qw_dit_packed_in_place_matches_input_major(dev, tmp_path):
+    """QwDit packs the projection weights in place (kh_pack_int8 + kh_copy); the blocks' output is bitwise the
+    one on the file's input-major bytes, and a packed weight is never handed out as KH_I8 again."""
+    from krea_image_amd import dit, kh, qw
+    path = str(tmp_path / "dit_q8.qw")
+    qw.write_random_dit(path, D=256, kv_heads=1, FF=512, layers=2, quant=True, seed=12)
+    print("[qw dit packed] D=256 layers=2", flush=True)
+    rng = np.random.default_rng(3)
+    txt = torch.from_numpy(rng.standard_normal((16, 256)).astype(np.float32)).to(dev)
+    z = torch.from_numpy(rng.standard_normal((80, 64)).astype(np.float32)).to(dev)
+    t = (0.5 * rng.standard_normal(256)).astype(np.float32)
+    tvec = (0.2 * rng.standard_normal(6 * 256)).astype(np.float32)
+    with qw.QwFile(path) as f:
+        f.upload()
+        outs = []
+        for pack in (False, True):
+            run = dit.QwDit(f, 16, 8, 10, dev, pack=pack)
+            assert all(L.up.w_dtype == (kh.I8P if pack else kh.I8) for L in run.layers)
+            run.set_cond(t, tvec)
+            vel = torch.empty(80, 64, device=dev)
+            run.forward(txt, z, vel)
+            torch.cuda.synchronize()
+            outs.append((run.x.cpu(), vel.cpu()))
+        # the residual stream after the blocks is bitwise equal; the velocity to rounding (the head's split-K
+        # gemm_f32 adds its partials with f32 atomics in no fixed order)
+        assert torch.equal(outs[0][0], outs[1][0])
+        assert rel_l2(outs[1][1].numpy(), outs[0][1].numpy()) <= 1e-5
+        assert f.weight("L0.gu").w_dtype == kh.I8P
+
+
 def test_qw_upload_places_every_tensor(dev, tmp_path):
     from krea_image_amd import kh, qw
     path = str(tmp_path / "w.qw")
