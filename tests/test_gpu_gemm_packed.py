@@ -114,3 +114,11 @@ def test_packed_rejections(dev):
         kh.gemv(x, W, y, 1, 256, 256, 256)
     with pytest.raises(kh.KhError, match="multiple of 8"):
         kh.pack_int8(torch.zeros(12, 64, dtype=torch.int8, device=dev))
+
+
+@pytest.mark.parametrize("epi,K,N", [("gelu", 3072, 12288), ("resid", 12288, 3072)], ids=["up", "down"])
+def test_packed_bitwise_benchmark_shapes(dev, epi, K, N):
+    """The bench's MLP pair at full size (4096 rows): packed == input-major, bitwise."""
+    print(f"[packed] bench shape {epi} M=4096 K={K} N={N}", flush=True)
+    a, b = _both(dev, O.F16, "ch", epi, 4096, N, K, seed=K + N)
+    assert torch.equal(a, b)
