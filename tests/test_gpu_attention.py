@@ -100,3 +100,23 @@ def test_attention_golden_fixture(dev):
 def test_attention_config3_rows(dev):
     """4608 tokens, 24 heads x 128, fp16; the oracle checks 3 heads' worth via a head subset."""
     run(dev, O.F16, 4608, 4608, 3, seed=8)
+
+
+def test_attention_rows_past_lq_untouched(dev):
+    """O rows >= Lq and the columns of other heads' slots past `heads` are never written: Lq = 300 ends inside
+    a 256-query workgroup, O carries 20 extra sentinel rows and 128 extra sentinel columns (ldo > 128 heads)."""
+    from krea_image_amd import kh
+    rng = np.random.default_rng(71)
+    Lq, Lk, H = 300, 200, 3
+    q = to_dev16(randn16(rng, (Lq, H * 128), O.F16), O.F16, dev)
+    k = to_dev16(randn16(rng, (Lk, H * 128), O.F16), O.F16, dev)
+    v = to_dev16(randn16(rng, (Lk, H * 128), O.F16), O.F16, dev)
+    ldo = (H + 1) * 128
+    Od = torch.full((Lq + 20, ldo), 3.0, dtype=torch.float16, device=dev)
+    print("[attention rows past Lq]", flush=True)
+    kh.attention(q, k, v, Od, Lq, Lk, H, H * 128, H * 128, H * 128, ldo)
+    torch.cuda.synchronize()
+    o = Od.cpu()
+    assert (o[Lq:] == 3.0).all(), "rows >= Lq were written"
+    assert (o[:Lq, H * 128:] == 3.0).all(), "columns past the last head were written"
+    assert torch.isfinite(o[:Lq, :H * 128].float()).all()

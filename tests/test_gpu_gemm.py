@@ -152,3 +152,25 @@ def test_gemm_golden_fixture_group128_bf16(dev):
             torch.from_numpy(g["s"]).to(dev), 128), C, M, N, K, K, N, N)
     torch.cuda.synchronize()
     assert rel_l2(C.cpu().float().numpy(), g["out_store16"]) < 8e-3
+
+
+@pytest.mark.parametrize("epi", ["store16", "resid_gate", "swiglu", "bias_f32"])
+@pytest.mark.parametrize("packed", [False, True])
+def test_gemm_rows_past_m_untouched(dev, epi, packed):
+    """Rows >= M of C are never written (gemm.metal:270,282): C is allocated with 37 extra rows of a sentinel;
+    M = 300 ends inside a 256-row tile, so the last tile's clamped rows must not store."""
+    from krea_image_amd import kh
+    rng = np.random.default_rng(61)
+    M, N, K, extra = 300, 512, 256, 37
+    A = to_dev16(randn16(rng, (M, K), O.F16), O.F16, dev)
+    W = weight_to_dev(make_weight(rng, K, N, "ch", O.F16), dev)
+    W = W.pack() if packed else W
+    vec = torch.from_numpy(rng.standard_normal(N).astype(np.float32)).to(dev)
+    ncol = N // 2 if epi == "swiglu" else N
+    dt = torch.float32 if epi in F32_OUT else torch.float16
+    C = torch.full((M + extra, ncol), 7.0, dtype=dt, device=dev)
+    print(f"[rows past M] epi={epi} packed={packed}", flush=True)
+    kh.gemm(epi, A, W, C, M, N, K, K, N, ncol, vec)
+    torch.cuda.synchronize()
+    assert (C[M:].cpu() == 7.0).all(), "rows >= M were written"
+    assert not (C[:M].cpu() == 7.0).all()
