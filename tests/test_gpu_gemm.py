@@ -174,3 +174,35 @@ def test_gemm_rows_past_m_untouched(dev, epi, packed):
     torch.cuda.synchronize()
     assert (C[M:].cpu() == 7.0).all(), "rows >= M were written"
     assert not (C[:M].cpu() == 7.0).all()
+
+
+def test_gemm_activation_offsets_near_2pow31(dev):
+    """Largest A the 32-bit activation offsets allow: (M - 1) * lda + K = 2146304000 < 2^31 (A is 4.3 GB of fp16).
+    Rows spread over the whole range, the last rows included, against the oracle; one row past the limit is
+    rejected."""
+    from krea_image_amd import kh
+    M, K, N = 262000, 8192, 256
+    g = torch.Generator(device=dev)
+    g.manual_seed(81)
+    print(f"[gemm max offsets] M={M} K={K} N={N}", flush=True)
+    A = torch.randn(M, K, generator=g, device=dev, dtype=torch.float16)
+    rng = np.random.default_rng(81)
+    wd = make_weight(rng, K, N, "ch", O.F16)
+    W = weight_to_dev(wd, dev).pack()
+    C = torch.empty(M, N, dtype=torch.float16, device=dev)
+    kh.gemm("store16", A, W, C, M, N, K, K, N, N)
+    torch.cuda.synchronize()
+    rows = np.concatenate([np.linspace(0, M - 9, 40).astype(np.int64), np.arange(M - 8, M)])
+    Ah = A[torch.from_numpy(rows).to(dev)].cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+    ref = O.to_f32(O.gemm(0, Ah, O.F16, wd["w"], O.I8, wd["s"], O.F16, K), O.F16)
+    got = C[torch.from_numpy(rows).to(dev)].cpu().float().numpy()
+    assert rel_l2(got, ref) <= TOL
+    del A, C
+    torch.cuda.empty_cache()
+    # 262145 rows: (M - 1) * lda + K = 2^31 + 8192, rejected before any launch (no buffers are touched)
+    import ctypes
+    err = ctypes.create_string_buffer(256)
+    wc = W.c()
+    rc = kh.load().kh_gemm(kh._stream(), 0, ctypes.c_void_p(16), 1, ctypes.byref(wc), ctypes.c_void_p(16), 262145, N,
+                           K, K, N, N, None, err, 256)
+    assert rc != 0 and "2^31" in err.value.decode()
