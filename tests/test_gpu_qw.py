@@ -71,6 +71,34 @@ def test_qw_dit_forward_matches_oracle(dev, tmp_path, big_gain):
         assert np.isfinite(got).all() and err <= TOL
 
 
+def test_qw_dit_28_layer_forward_within_budget(dev, tmp_path):
+    """A full-depth forward (the reference's 28 blocks, narrow width) from a dit_q8-format file against the
+    oracle's composition: the per-forward budget of 1.6 % relative L2 holds with the error accumulated over all
+    layers, not just over one or two."""
+    from krea_image_amd import dit, qw
+    path = str(tmp_path / "dit28.qw")
+    qw.write_random_dit(path, D=256, kv_heads=1, FF=512, layers=28, quant=True, seed=13, big_gain=(9, 17, 20.0))
+    print("[qw dit 28 layers] D=256 heads=2/1 ff=512", flush=True)
+    with qw.QwFile(path) as f:
+        f.upload()
+        run = dit.QwDit(f, 16, 8, 10, dev)
+        big = [L.big_dim for L in run.layers]
+        rng = np.random.default_rng(5)
+        txt = rng.standard_normal((16, 256)).astype(np.float32)
+        z = rng.standard_normal((80, 64)).astype(np.float32)
+        t = (0.5 * rng.standard_normal(256)).astype(np.float32)
+        tvec = (0.2 * rng.standard_normal(6 * 256)).astype(np.float32)
+        run.set_cond(t, tvec)
+        vel = torch.empty(80, 64, device=dev)
+        run.forward(torch.from_numpy(txt).to(dev), torch.from_numpy(z).to(dev), vel)
+        torch.cuda.synchronize()
+        got = vel.cpu().numpy()
+        ref = oracle_forward(f, run.shape, big, txt, z, t, tvec, run.cos.cpu().numpy(), run.sin.cpu().numpy())
+        err = rel_l2(got, ref)
+        print(f"    28-layer velocity rel_l2={err:.3e}", flush=True)
+        assert np.isfinite(got).all() and err <= TOL
+
+
 def test_qw_dit_packed_in_place_matches_input_major(dev, tmp_path):
     """QwDit packs the projection weights in place (kh_pack_int8 + kh_copy); the blocks' output is bitwise the
     one on the file's input-major bytes, and a packed weight is never handed out as KH_I8 again."""
