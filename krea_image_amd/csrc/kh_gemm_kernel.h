@@ -11,10 +11,12 @@
 //    accumulator holds 4 consecutive output columns n of one row m: epilogue loads of scale / bias / gate
 //    and the 16-bit or f32 stores are 8- or 16-byte vectors.
 //  * Both tiles live in LDS as [row][64 k] 16-bit with the 16-byte chunk index XOR-swizzled by swz(row),
-//    so the MFMA operand reads (one ds_read_b128 per lane: 8 consecutive k of one row) are conflict-free.
+//    so the MFMA operand reads (one ds_read_b128 per lane: 8 consecutive k of one row) are conflict-free
+//    (gfx950 LDS: 32 banks x 4 B, 8 lanes of a 16-byte access per cycle).
 //  * Activations stream global -> LDS by DMA (global_load_lds, no VGPR staging) through a 3-stage ring.
 //  * Weights: each thread loads 8 k-rows x 4 n-columns two K steps ahead (a dword per int8 row, coalesced
-//    256 B per wave and row; inline-asm loads with explicit waits), and converts them to 16-bit while
+//    256 B per wave and row, or with WF_PK the same 32 bytes as two 16-byte loads from kh_pack_int8's
+//    layout; inline-asm loads with explicit waits), and converts them to 16-bit while
 //    transposing them in registers (v_perm_b32) into four 16-byte k-vectors, stored to a 2-stage LDS ring
 //    between the MFMA slices:
 //      - int8 per-channel, fp16 activations: 0x6400 | (q ^ 0x80) is the fp16 value 1024 + q + 128, so one
