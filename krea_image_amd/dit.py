@@ -165,6 +165,17 @@ class DitRunner:
                                    self.sin.data_ptr(), self.qbig.data_ptr(), self.kbig.data_ptr())
         self._cfg = shape.config()
 
+    def sibling(self, T: int) -> "DitRunner":
+        """A runner over the same weights, embed / head and conditioning at another text length (the negative
+        prompt of classifier-free guidance, engine/src/pipeline.mm:304-308): its own activation buffers and
+        RoPE tables. The conditioning (cond, tvec) is copied now; refresh it if the step changes it."""
+        r = DitRunner(self.shape, T, self.H, self.W, self.dev, layers=self.layers)
+        for name in ("first_w", "first_b", "last_w", "last_b", "fin_mul", "fin_add"):
+            setattr(r, name, getattr(self, name))
+        r.tvec.copy_(self.tvec)
+        r.cond.copy_(self.cond)
+        return r
+
     def run_layers(self, l0: int = 0, l1: Optional[int] = None):
         """DiT::run_layers (engine/src/model.mm:519-525) through kh_dit_forward."""
         l1 = len(self.layers) if l1 is None else l1
@@ -188,15 +199,23 @@ class DitRunner:
         return vel
 
     def denoise(self, txt: torch.Tensor, z: torch.Tensor, sig, vel: Optional[torch.Tensor] = None,
-                before_step=None):
-        """The denoising loop of engine/src/pipeline.mm:300-316 without guidance or masks: for each step i,
-        velocity = forward(txt, z), then z += (sig[i + 1] - sig[i]) velocity (kh_euler_step), in place on z.
-        before_step(i), if given, runs first in each step (e.g. QwDit.set_cond for the step's noise level)."""
+                before_step=None, neg: Optional["DitRunner"] = None, ntxt: Optional[torch.Tensor] = None,
+                cfg_scale: float = 0.0):
+        """The denoising loop of engine/src/pipeline.mm:300-316 (without masks): for each step i, velocity =
+        forward(txt, z); with guidance (neg: a runner over the same layers at the negative prompt's length,
+        ntxt its text rows), vel2 = neg.forward(ntxt, z) first and vel += cfg_scale (vel - vel2)
+        (kh_cfg_combine); then z += (sig[i + 1] - sig[i]) vel (kh_euler_step), in place on z. before_step(i),
+        if given, runs first in each step (e.g. QwDit.set_cond for the step's noise level)."""
         vel = torch.empty_like(z) if vel is None else vel
+        vel2 = torch.empty_like(z) if neg is not None else None
         for i in range(len(sig) - 1):
             if before_step is not None:
                 before_step(i)
+            if neg is not None:
+                neg.forward(ntxt, z, vel2)
             self.forward(txt, z, vel)
+            if neg is not None:
+                kh.cfg_combine(vel, vel2, cfg_scale)
             kh.euler_step(z, vel, float(sig[i + 1]) - float(sig[i]))
         return z
 

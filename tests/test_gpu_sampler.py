@@ -79,3 +79,37 @@ def test_denoise_loop_matches_host_updates(dev):
     r = (zr - z0).cpu().numpy()
     assert rel_l2(d, r) <= 1e-4
     assert not torch.equal(z.cpu(), z0.cpu())
+
+
+def test_denoise_loop_with_guidance(dev):
+    """pipeline.mm:300-316 with classifier-free guidance: the negative prompt's forward (a sibling runner at
+    another text length over the same weights), kh_cfg_combine, then the Euler step; against the same loop
+    with both updates done by the oracle on the host (to rounding: the forward's adaLN GEMV uses atomics)."""
+    from krea_image_amd import dit, kh
+    shape = small_shapes()["baseline"]
+    shape.layers = 2
+    run = dit.DitRunner(shape, 16, 8, 10, dev, seed=9)
+    neg = run.sibling(8)
+    g = torch.Generator(device=dev)
+    g.manual_seed(10)
+    txt = torch.randn(16, shape.dim, generator=g, device=dev)
+    ntxt = torch.randn(8, shape.dim, generator=g, device=dev)
+    z0 = torch.randn(80, 64, generator=g, device=dev)
+    sig = kh.sigmas(2)
+    print("[denoise cfg] 2 steps, scale 3.5", flush=True)
+    z = run.denoise(txt, z0.clone(), sig, neg=neg, ntxt=ntxt, cfg_scale=3.5)
+    zr = z0.clone()
+    v, v2 = torch.empty_like(zr), torch.empty_like(zr)
+    for i in range(2):
+        neg.forward(ntxt, zr, v2)
+        run.forward(txt, zr, v)
+        torch.cuda.synchronize()
+        vc = O.cfg_combine(v.cpu().numpy(), v2.cpu().numpy(), np.float32(3.5))
+        upd = O.euler_step(zr.cpu().numpy(), vc, np.float32(float(sig[i + 1]) - float(sig[i])))
+        zr = torch.from_numpy(upd).to(dev)
+    torch.cuda.synchronize()
+    assert torch.isfinite(z).all()
+    assert rel_l2((z - z0).cpu().numpy(), (zr - z0).cpu().numpy()) <= 1e-4
+    # guidance changes the result
+    zn = run.denoise(txt, z0.clone(), sig)
+    assert rel_l2((zn - z0).cpu().numpy(), (z - z0).cpu().numpy()) > 1e-3
