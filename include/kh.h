@@ -9,8 +9,9 @@
  * launch error; `err` (if non-NULL) receives a NUL-terminated message of at most errlen bytes, the
  * convention of the reference's C ABI (engine/src/krea.h:57-73, engine/src/pipeline.mm:594-641).
  *
- * Ops are asynchronous on `stream` (a hipStream_t; NULL = the null stream). Ops do not allocate, with one
- * exception: kh_gemm keeps a per-(device, stream) stream-K workspace (see kh_gemm).
+ * Ops are asynchronous on `stream` (a hipStream_t; NULL = the null stream). Ops never allocate device memory:
+ * what an op needs beyond its inputs and outputs comes from the caller (workspace arguments), as the
+ * reference's ops take buffers owned by the model (engine/src/model.mm:251-267).
  */
 #ifndef KH_H
 #define KH_H
@@ -64,11 +65,8 @@ typedef struct kh_weight {
  * `epi`. vec: f32 [N] gate (RESID_GATE) or bias (BIAS16 / BIAS_F32), else unused. C row stride ldc in
  * elements of the output type. Constraints: M > 0, N % 64 == 0, K % 64 == 0, int8 group a power of two
  * >= 64 dividing K, 16-byte aligned A / W rows (lda % 8 == 0, ldw % 16 == 0 for int8, % 8 for 16-bit).
- * Shapes whose 256 x 256 tiles would fill under 60 % of a wave of workgroups run stream-K (the tiles' K
- * steps spread over one workgroup per CU); those launches use a workspace of 2 x CUs x 256 KiB + 256 KiB
- * that kh_gemm allocates once per (device, stream) on first need and keeps until the process ends (on a
- * capturing stream without one, the launch stays data-parallel). Results are deterministic either way.
- * KH_GEMM_STREAMK=0 in the environment keeps every launch data-parallel. Data-parallel launches may use
+ * kh_gemm launches are data-parallel (one output tile per workgroup); kh_gemm_ws below adds stream-K for shapes
+ * that would leave CUs idle. Data-parallel launches may use
  * narrower tiles (not for SWIGLU): 256 x 192 where N pads less to 192 than to 256 (e.g. 384) or where
  * 256-wide tiles fill only part of one wave of workgroups and 192-wide ones still fit in one (4096 x 3072);
  * 256 x 128 for 16-bit weights where N pads less to 128 (e.g. 64, 128). KH_GEMM_TN192=0 keeps 256-wide
@@ -76,6 +74,24 @@ typedef struct kh_weight {
  * Replaces krea::Metal::gemm (engine/src/metal.h:66-69, engine/src/metal.mm:146-163). */
 int kh_gemm(kh_stream stream, int epi, const void* A, int a_dtype, const kh_weight* W, void* C, int M, int N, int K,
             int lda, int ldw, int ldc, const void* vec, char* err, int errlen);
+
+/* kh_gemm with a stream-K workspace: shapes whose 256 x 256 tiles would fill under 60 % of a wave of workgroups
+ * (e.g. 1536 x 12288 outputs on 256 CUs) spread the tiles' K steps over one workgroup per CU; a workgroup that
+ * covers part of a tile stores its f32 partial in the workspace and the last to arrive adds the partials in K
+ * order (deterministic). workspace: device memory of >= kh_gemm_workspace_bytes() bytes (2 x CUs x 256 KiB of
+ * partial slots + 16 KiB of arrival counters), 256-byte aligned, prepared once by kh_gemm_workspace_init (it
+ * zeroes the counters; every launch leaves them zero again). Launches that share a workspace must be ordered
+ * (one stream). A NULL or smaller workspace, or KH_GEMM_STREAMK=0 in the environment, gives the data-parallel
+ * launch of kh_gemm. Stream-K and data-parallel launches of one GEMM agree to fp32 rounding (the K sum is split
+ * differently). The workspace is the caller-owned arena the reference's model keeps for its ops
+ * (engine/src/model.mm:251-267, engine/src/metal.mm:146-163). */
+int kh_gemm_ws(kh_stream stream, int epi, const void* A, int a_dtype, const kh_weight* W, void* C, int M, int N, int K,
+               int lda, int ldw, int ldc, const void* vec, void* workspace, size_t workspace_bytes, char* err,
+               int errlen);
+/* Workspace size kh_gemm_ws uses on the current device (0 if no device). */
+size_t kh_gemm_workspace_bytes(void);
+/* Prepares a kh_gemm_ws workspace (a fill kernel on `stream`, so it may be captured in a graph). */
+int kh_gemm_workspace_init(kh_stream stream, void* workspace, size_t workspace_bytes, char* err, int errlen);
 
 /* Load-time rearrangement of int8 weights Wt[K, ldw] (row stride ldw bytes) into the packed layout kh_gemm reads
  * as w_dtype KH_I8P: element (k, n) at byte (k / 8) 8 ldw + 32 (n / 4) + 4 (k % 8) + n % 4, i.e. 8-row panels in
@@ -118,16 +134,20 @@ int kh_qk_norm_rope(kh_stream stream, void* qkv, int dtype, const float* wq, con
  * pass reads), so the q / k heads never make a round trip through HBM. Arguments as for the two calls, with
  * the projection output C in place of qkv (rows = M, ld = ldc); q_off and k_off multiples of 128; norm
  * weights and tables 16-byte aligned. The per-head sum of squares is added in a different order than the
- * separate pass (results agree to rounding). Replaces the pair Metal::gemm(Epi::BF16) + Metal::qk_norm_rope of
+ * separate pass (results agree to rounding). workspace / workspace_bytes: as for kh_gemm_ws (NULL: data-parallel).
+ * Replaces the pair Metal::gemm(Epi::BF16) + Metal::qk_norm_rope of
  * DiT::layer (engine/src/model.mm:373-375). */
 int kh_gemm_qk_norm_rope(kh_stream stream, const void* A, int a_dtype, const kh_weight* W, void* C, int M, int N,
                          int K, int lda, int ldw, int ldc, const float* wq, const float* wk, const float* cosb,
                          const float* sinb, int q_off, int n_q, int k_off, int n_k, float eps, int rope_mode,
-                         int big_dim, float* qbig, float* kbig, char* err, int errlen);
+                         int big_dim, float* qbig, float* kbig, void* workspace, size_t workspace_bytes, char* err,
+                         int errlen);
 
-/* adaLN modulation GEMV: y[r, n] = (y[r, n] if act & 2) + sum_k act1(x[r, k]) W~[k, n] + bias[n] (bias may be
- * NULL), act & 1 = SiLU on load; rows 1..4, x [rows, K] / y [rows, N] f32, W as in kh_gemm (int8 per-channel or
- * group, or 16-bit). Column sums are combined with f32 atomics (summation order not fixed).
+/* adaLN / conditioning GEMV: y[r, n] = (y[r, n] if act & 2) + bias[n] + sum_k act1(x[r, k]) W~[k, n] (bias may be
+ * NULL); act & 1 = SiLU on load, act & 4 = GELU(tanh) on load (exclusive); rows 1..4, x [rows, K] / y [rows, N]
+ * f32; W as in kh_gemm (int8 per-channel or group, or 16-bit) or f32 (w_dtype KH_F32). N a multiple of 16 (int8),
+ * 8 (16-bit) or 4 (f32); weight rows 16-byte aligned. Each output is summed in a fixed order (no atomics): the
+ * same inputs give the same bits on every run.
  * Replaces the gemv_bf16 kernel (engine/kernels/gemm.metal:346-371) and the CPU cblas_sgemv of
  * Conditioning::compute (engine/src/model.mm:571-591). */
 int kh_gemv(kh_stream stream, const float* x, const kh_weight* W, float* y, int rows, int N, int K, int ldw, int act,
@@ -138,8 +158,15 @@ int kh_gemv(kh_stream stream, const float* x, const kh_weight* W, float* y, int 
 int kh_make_cond(kh_stream stream, const float* tvec, const float* table, const float* n1, const float* n2, int D,
                  float* mods, char* err, int errlen);
 
+/* Final-norm vectors of the head from the step's t: fin[k] = nf[k] (1 + t[k] + lin[k]), fin[D + k] = t[k] + lin[D + k]
+ * (t [D], lin = last.mod [2 D], nf = last.n [D], fin [2 D], all f32). The fin half of DiT::make_cond
+ * (engine/src/model.mm:340-346). */
+int kh_make_fin(kh_stream stream, const float* t, const float* lin, const float* nf, int D, float* fin, char* err,
+                int errlen);
+
 /* fp32 GEMM (patch embed / final projection): C = A[M,K] x W[K,N] with mode bit 0 + bias[N], bit 1 GELU(tanh),
- * bit 2 accumulate into C. Replaces krea::Metal::gemm_f32 (engine/src/metal.h:70-71, f32gemm.metal). */
+ * bit 2 accumulate into C; every output summed over K in order by one thread (results repeat bit for bit).
+ * Replaces krea::Metal::gemm_f32 (engine/src/metal.h:70-71, f32gemm.metal). */
 int kh_gemm_f32(kh_stream stream, const float* A, const float* W, float* C, int M, int N, int K, int lda, int ldw,
                 int ldc, int mode, const float* bias, char* err, int errlen);
 
@@ -209,6 +236,8 @@ typedef struct kh_dit_state { /* device buffers, owned by the caller; rows R = t
   const float* sinb;
   float* qbig;        /* [R, heads] (layers with big_dim >= 0) */
   float* kbig;        /* [R, kv_heads] */
+  void* gemm_ws;      /* kh_gemm_ws workspace for the layer's GEMMs (prepared by kh_gemm_workspace_init), or NULL */
+  size_t gemm_ws_bytes;
 } kh_dit_state;
 
 /* One layer: adaLN (GEMV + make_cond) -> norm -> qkv GEMM -> QK norm + RoPE -> attention -> O GEMM with gated
@@ -248,6 +277,16 @@ int kh_qw_find(const kh_qw* f, const char* name, kh_qw_tensor* out); /* KH_EINVA
 /* Synchronous: returns once the data is resident on the current device. Idempotent. */
 int kh_qw_upload(kh_qw* f, kh_stream stream, char* err, int errlen);
 
+/* Timestep conditioning of one step: t [D] and tvec [6 D] (f32, device) for noise level sigma from an uploaded
+ * cond.qw (tools/convert.py:287-308). Conditioning::get (engine/src/model.mm:545-569): a sigma equal to an
+ * entry of the `base.` (fast = 0) or `fast.` (fast = 1) table copies that row; fast = 1 without a match fails
+ * (KH_EINVAL, the reference's message). Otherwise Conditioning::compute (model.mm:571-591): e = [cos | sin](
+ * bf16(sigma) 1000 10000^(-i/128)), i < 128, on the host; then on the device h = tmlp1(e), t = tmlp2(gelu(h)),
+ * tvec = tproj(gelu(t)) as f32 GEMVs (kh_gemv, GELU on load). work: device f32 scratch of >= 256 + D floats
+ * (unused on a table hit). *from_table (may be NULL) = 1 on a table hit, else 0. Stream-ordered. */
+int kh_conditioning(kh_stream stream, const kh_qw* cond, int fast, float sigma, float* t, float* tvec, float* work,
+                    size_t work_bytes, int* from_table, char* err, int errlen);
+
 /* ---- runtime surface around the ops (Metal::alloc / begin / wait, engine/src/metal.h:53-60) ---- */
 int kh_stream_create(kh_stream* out, char* err, int errlen);  /* non-blocking stream, default priority */
 int kh_stream_destroy(kh_stream s);
@@ -267,9 +306,11 @@ int kh_copy(kh_stream s, void* dst, const void* src, size_t bytes, char* err, in
  * activation type (dtype KH_F16 / KH_BF16), rows >= 9 C (up to K, a multiple of 64) are multiplied by zero
  * activations; bias f32 [N]; res (NULL or 16-bit [H W, ldy], the residual, added after the biased output is
  * rounded to 16 bits, then rounded again); y [H W, ldy]. C, ldx, ldy multiples of 8, N of 64; 16-byte aligned.
+ * workspace / workspace_bytes: the GEMM's stream-K workspace, as for kh_gemm_ws (NULL: data-parallel).
  * Replaces VAEDecoder::conv mode 3 (engine/src/vae.mm:112-125, kernels/vae.metal vconv3x3). */
 int kh_vae_conv3x3(kh_stream stream, const void* x, int ldx, int C, int H, int W, int up, int dtype, const kh_weight* Wt,
-                   int K, int N, const float* bias, const void* res, void* y, int ldy, char* err, int errlen);
+                   int K, int N, const float* bias, const void* res, void* y, int ldy, void* workspace,
+                   size_t workspace_bytes, char* err, int errlen);
 /* Sub-pixel weights of a nearest-2x upsample + 3x3 conv (the reference's vae_subpix_weights,
  * engine/kernels/vae.metal:134-160, driven by engine/src/vae.mm:137-150): W [9 Cin, Cout] 16-bit (dtype) ->
  * W2 [K, 4 Np] with W2[(2r + s) Cin + ci, (2py + px) Np + co] = 16-bit round of the fp32 sum of the 3x3 taps that
@@ -279,10 +320,12 @@ int kh_vae_subpix_weights(kh_stream stream, const void* W, int dtype, int Cin, i
                           const float* bias, float* bias4, char* err, int errlen);
 /* y = conv3x3(nearest2x(x)) + bias as 4 sub-pixel 2x2 convs in one implicit GEMM (4/9 of the direct form's
  * multiply-adds): x NHWC [H W, ldx] with C channels (the low-res image), W2 / bias4 from
- * kh_vae_subpix_weights, y [2H x 2W pixels, ldy] with Np channels (Np a multiple of 128 or 192). Replaces
+ * kh_vae_subpix_weights, y [2H x 2W pixels, ldy] with Np channels (Np a multiple of 128 or 192); workspace as for
+ * kh_vae_conv3x3. Replaces
  * VAEDecoder::conv mode 2 (engine/src/vae.mm:137-150, vconv_up2). */
 int kh_vae_conv_up2(kh_stream stream, const void* x, int ldx, int C, int H, int W, int dtype, const kh_weight* W2, int K,
-                    int Np, const float* bias4, void* y, int ldy, char* err, int errlen);
+                    int Np, const float* bias4, void* y, int ldy, void* workspace, size_t workspace_bytes, char* err,
+                    int errlen);
 /* 3x3 (zero padding 1) im2col of output pixels [m0, m0 + rows) of an H x W output: col[r, tap * C + ci],
  * columns [9 C, Kpad) zero; up = 1: x is H/2 x W/2 and nearest-upsampled (the vconv A loader,
  * engine/kernels/vae.metal:11-28). C, ldx, Kpad multiples of 8. */
@@ -305,8 +348,8 @@ int kh_vae_conv_out(kh_stream stream, const void* x, int ldx, int C, const void*
 size_t kh_vae_workspace_bytes(int H16, int W16);
 /* Full decode (VAEDecoder::run, engine/src/vae.mm:289-337): z f32 [H16 W16, 64] -> rgba uint8 [16 H16 x 16 W16, 4]
  * on the device. Weights come from an uploaded vae.qw (kh_qw_upload), by the converter's tensor names. The
- * workspace (256-byte aligned, >= kh_vae_workspace_bytes) holds every intermediate; the only allocation is the
- * GEMM stream-K workspace of kh_gemm, made once per stream. */
+ * workspace (256-byte aligned, >= kh_vae_workspace_bytes) holds every intermediate and the GEMMs' stream-K
+ * workspace; nothing is allocated. */
 int kh_vae_decode(kh_stream stream, const kh_qw* vae, const float* z, int H16, int W16, void* workspace,
                   size_t workspace_bytes, void* rgba, char* err, int errlen);
 

@@ -13,6 +13,24 @@ int kh_gemm(kh_stream stream, int epi, const void* A, int a_dtype, const kh_weig
   return kh::gemm((hipStream_t)stream, epi, A, a_dtype, *W, C, M, N, K, lda, ldw, ldc, vec, e);
 }
 
+int kh_gemm_ws(kh_stream stream, int epi, const void* A, int a_dtype, const kh_weight* W, void* C, int M, int N, int K,
+               int lda, int ldw, int ldc, const void* vec, void* workspace, size_t workspace_bytes, char* err,
+               int errlen) {
+  kh::Err e{err, errlen};
+  e.clear();
+  if (!W) return e.fail("gemm: null weight descriptor");
+  const kh::GemmWs ws{workspace, workspace_bytes};
+  return kh::gemm((hipStream_t)stream, epi, A, a_dtype, *W, C, M, N, K, lda, ldw, ldc, vec, e, &ws);
+}
+
+size_t kh_gemm_workspace_bytes(void) { return kh::gemm_workspace_bytes(); }
+
+int kh_gemm_workspace_init(kh_stream stream, void* workspace, size_t workspace_bytes, char* err, int errlen) {
+  kh::Err e{err, errlen};
+  e.clear();
+  return kh::gemm_workspace_init((hipStream_t)stream, workspace, workspace_bytes, e);
+}
+
 int kh_pack_int8(kh_stream stream, const void* W, int K, int ldw, void* out, char* err, int errlen) {
   kh::Err e{err, errlen};
   e.clear();
@@ -38,12 +56,14 @@ int kh_rms_norm(kh_stream stream, const float* x, const float* mul, const float*
 int kh_gemm_qk_norm_rope(kh_stream stream, const void* A, int a_dtype, const kh_weight* W, void* C, int M, int N,
                          int K, int lda, int ldw, int ldc, const float* wq, const float* wk, const float* cosb,
                          const float* sinb, int q_off, int n_q, int k_off, int n_k, float eps, int rope_mode,
-                         int big_dim, float* qbig, float* kbig, char* err, int errlen) {
+                         int big_dim, float* qbig, float* kbig, void* workspace, size_t workspace_bytes, char* err,
+                         int errlen) {
   kh::Err e{err, errlen};
   e.clear();
   if (!W) return e.fail("gemm_qk_norm_rope: null weight descriptor");
   const kh::QkNormRope q{wq, wk, cosb, sinb, qbig, kbig, q_off, n_q, k_off, n_k, rope_mode, big_dim, eps};
-  return kh::gemm_qk_norm_rope((hipStream_t)stream, A, a_dtype, *W, C, M, N, K, lda, ldw, ldc, q, e);
+  const kh::GemmWs ws{workspace, workspace_bytes};
+  return kh::gemm_qk_norm_rope((hipStream_t)stream, A, a_dtype, *W, C, M, N, K, lda, ldw, ldc, q, e, &ws);
 }
 
 int kh_qk_norm_rope(kh_stream stream, void* qkv, int dtype, const float* wq, const float* wk, const float* cosb,
@@ -68,6 +88,20 @@ int kh_make_cond(kh_stream stream, const float* tvec, const float* table, const 
   kh::Err e{err, errlen};
   e.clear();
   return kh::make_cond((hipStream_t)stream, tvec, table, n1, n2, D, mods, e);
+}
+
+int kh_make_fin(kh_stream stream, const float* t, const float* lin, const float* nf, int D, float* fin, char* err,
+                int errlen) {
+  kh::Err e{err, errlen};
+  e.clear();
+  return kh::make_fin((hipStream_t)stream, t, lin, nf, D, fin, e);
+}
+
+int kh_conditioning(kh_stream stream, const kh_qw* cond, int fast, float sigma, float* t, float* tvec, float* work,
+                    size_t work_bytes, int* from_table, char* err, int errlen) {
+  kh::Err e{err, errlen};
+  e.clear();
+  return kh::conditioning((hipStream_t)stream, cond, fast, sigma, t, tvec, work, work_bytes, from_table, e);
 }
 
 int kh_gemm_f32(kh_stream stream, const float* A, const float* W, float* C, int M, int N, int K, int lda, int ldw,
@@ -113,11 +147,13 @@ int kh_dit_forward(kh_stream stream, const kh_dit_config* cfg, const kh_dit_laye
 
 /* ---- VAE decoder ---- */
 int kh_vae_conv3x3(kh_stream stream, const void* x, int ldx, int C, int H, int W, int up, int dtype, const kh_weight* Wt,
-                   int K, int N, const float* bias, const void* res, void* y, int ldy, char* err, int errlen) {
+                   int K, int N, const float* bias, const void* res, void* y, int ldy, void* workspace,
+                   size_t workspace_bytes, char* err, int errlen) {
   kh::Err e{err, errlen};
   e.clear();
   if (!Wt) return e.fail("conv3x3: null weight descriptor");
-  return kh::conv3x3((hipStream_t)stream, x, ldx, C, H, W, up, dtype, *Wt, K, N, bias, res, y, ldy, e);
+  const kh::GemmWs ws{workspace, workspace_bytes};
+  return kh::conv3x3((hipStream_t)stream, x, ldx, C, H, W, up, dtype, *Wt, K, N, bias, res, y, ldy, e, &ws);
 }
 
 int kh_vae_subpix_weights(kh_stream stream, const void* W, int dtype, int Cin, int Cout, void* W2, int K, int Np,
@@ -128,11 +164,13 @@ int kh_vae_subpix_weights(kh_stream stream, const void* W, int dtype, int Cin, i
 }
 
 int kh_vae_conv_up2(kh_stream stream, const void* x, int ldx, int C, int H, int W, int dtype, const kh_weight* W2, int K,
-                    int Np, const float* bias4, void* y, int ldy, char* err, int errlen) {
+                    int Np, const float* bias4, void* y, int ldy, void* workspace, size_t workspace_bytes, char* err,
+                    int errlen) {
   kh::Err e{err, errlen};
   e.clear();
   if (!W2) return e.fail("conv_up2: null weight descriptor");
-  return kh::conv_up2_subpix((hipStream_t)stream, x, ldx, C, H, W, dtype, *W2, K, Np, bias4, y, ldy, e);
+  const kh::GemmWs ws{workspace, workspace_bytes};
+  return kh::conv_up2_subpix((hipStream_t)stream, x, ldx, C, H, W, dtype, *W2, K, Np, bias4, y, ldy, e, &ws);
 }
 
 int kh_vae_im2col(kh_stream stream, const void* x, int ldx, int C, int H, int W, int up, int m0, int rows, void* col,

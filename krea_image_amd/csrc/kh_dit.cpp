@@ -1,7 +1,7 @@
 // Host-side DiT block orchestration on one HIP stream: engine/src/model.mm:369-385 (DiT::layer) and
 // engine/src/model.mm:519-525 (DiT::run_layers), with the adaLN modulation (Conditioning::compute +
 // DiT::make_cond, engine/src/model.mm:317-347 and 571-591) moved onto the GPU as a GEMV + make_cond.
-// Everything is enqueued asynchronously; nothing allocates.
+// Everything is enqueued asynchronously; nothing allocates (the GEMMs' stream-K workspace is state->gemm_ws).
 #include <cmath>
 
 #include "kh_internal.h"
@@ -34,6 +34,7 @@ int dit_layer_forward(hipStream_t st, const kh_dit_config& c, const kh_dit_layer
   const int nup = c.mlp == 1 ? 2 * c.ff : c.ff;
   const size_t es = elem_size(c.dtype);
   char* qkv = (char*)s.qkv;
+  const GemmWs ws{s.gemm_ws, s.gemm_ws_bytes};
 
   // adaLN: tvec = SiLU(cond) W_ada + b; mods = make_cond(tvec, table, n1, n2)
   if (L.ada.w) {
@@ -52,7 +53,7 @@ int dit_layer_forward(hipStream_t st, const kh_dit_config& c, const kh_dit_layer
   // QKV projection, then the per-head q / k RMSNorm + RoPE as its own HBM-bound pass (model.mm:373-375). The
   // fused form (gemm_qk_norm_rope) measured slower at 4608 rows: 304 us against 264 + 25 us, because the GEMM
   // epilogue runs with the MFMAs idle and its per-row table loads are latency-bound there.
-  if ((rc = gemm(st, KH_EPI_STORE16, s.h, c.dtype, L.qkv, s.qkv, R, nqkv, D, D, nqkv, nqkv, nullptr, e))) return rc;
+  if ((rc = gemm(st, KH_EPI_STORE16, s.h, c.dtype, L.qkv, s.qkv, R, nqkv, D, D, nqkv, nqkv, nullptr, e, &ws))) return rc;
   if ((rc = qk_norm_rope(st, s.qkv, c.dtype, L.qn, L.kn, s.cosb, s.sinb, R, nqkv, 0, c.heads, D, c.kv_heads, c.eps,
                          c.rope_mode, L.big_dim, s.qbig, s.kbig, e)))
     return rc;
@@ -61,13 +62,13 @@ int dit_layer_forward(hipStream_t st, const kh_dit_config& c, const kh_dit_layer
                       c.heads / c.kv_heads, 0, 0, c.attn_gate ? qkv + (D + 2 * kvD) * es : nullptr,
                       c.attn_gate ? nqkv : 0, big ? s.qbig : nullptr, big ? s.kbig : nullptr, e)))
     return rc;
-  if ((rc = gemm(st, KH_EPI_RESID_GATE, s.ao, c.dtype, L.o, s.x, R, D, D, D, D, D, m + 2 * D, e))) return rc;
+  if ((rc = gemm(st, KH_EPI_RESID_GATE, s.ao, c.dtype, L.o, s.x, R, D, D, D, D, D, m + 2 * D, e, &ws))) return rc;
   // MLP half
   if ((rc = rms_norm(st, s.x, m + 3 * D, m + 4 * D, s.h, c.dtype, R, D, D, D, c.eps, c.norm_center, e))) return rc;
   if ((rc = gemm(st, c.mlp == 1 ? KH_EPI_SWIGLU : KH_EPI_GELU, s.h, c.dtype, L.up, s.mid, R, nup, D, D, nup, c.ff,
-                 nullptr, e)))
+                 nullptr, e, &ws)))
     return rc;
-  return gemm(st, KH_EPI_RESID_GATE, s.mid, c.dtype, L.down, s.x, R, D, c.ff, c.ff, D, D, m + 5 * D, e);
+  return gemm(st, KH_EPI_RESID_GATE, s.mid, c.dtype, L.down, s.x, R, D, c.ff, c.ff, D, D, m + 5 * D, e, &ws);
 }
 
 int dit_forward(hipStream_t st, const kh_dit_config& c, const kh_dit_layer* layers, int n, const kh_dit_state& s,

@@ -15,19 +15,14 @@ namespace {
 
 using namespace gemm_detail;
 
-// ---- stream-K workspace: per (device, stream), allocated on first use and kept until the process ends.
-//      Launches on one stream are ordered, so one workspace per stream is race-free. ----
-constexpr int SK_MAX_TILES = 1 << 16;
-constexpr int SK_MIN_ITERS = 4;  // below this many K steps per workgroup the partial traffic dominates
-
-struct SkWorkspace {
-  float* ws = nullptr;
-  int* cnt = nullptr;
-  int ctas = 0;
-};
+// ---- stream-K workspace: caller-owned device memory (kh_gemm_ws / the DiT and VAE workspaces), never allocated
+//      here. Layout: 2 partial-tile slots of BM x BN f32 per workgroup of one wave, then SK_MAX_TILES arrival
+//      counters (zero between launches: the finishing workgroup of a tile resets its counter). Launches that
+//      share one workspace must be ordered (one stream). ----
+constexpr int SK_MAX_TILES = 4096;  // stream-K runs only below 60 % of two waves: < 1.2 x CUs tiles
+constexpr int SK_MIN_ITERS = 4;     // below this many K steps per workgroup the partial traffic dominates
 
 std::mutex sk_mu;
-std::map<std::pair<int, hipStream_t>, SkWorkspace> sk_map;
 std::map<int, int> sk_ctas;  // device -> workgroups of one full wave (one per CU), a multiple of 8
 
 // KH_GEMM_STREAMK=0 keeps every launch data-parallel (read per call, so a host can switch it at run time)
@@ -48,30 +43,7 @@ int sk_cta_count(int dev) {
   return c;
 }
 
-const SkWorkspace* sk_workspace(int dev, hipStream_t st, int ctas) {
-  std::lock_guard<std::mutex> lk(sk_mu);
-  auto key = std::make_pair(dev, st);
-  auto it = sk_map.find(key);
-  if (it != sk_map.end()) return it->second.ws ? &it->second : nullptr;
-  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(st, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return nullptr;
-  SkWorkspace w;
-  w.ctas = ctas;
-  const size_t ws_bytes = (size_t)2 * ctas * BM * BN * sizeof(float);
-  if (hipMalloc((void**)&w.ws, ws_bytes) != hipSuccess) w.ws = nullptr;
-  if (w.ws && hipMalloc((void**)&w.cnt, SK_MAX_TILES * sizeof(int)) != hipSuccess) {
-    (void)hipFree(w.ws);
-    w.ws = nullptr;
-  }
-  if (w.ws && hipMemset(w.cnt, 0, SK_MAX_TILES * sizeof(int)) != hipSuccess) {
-    (void)hipFree(w.ws);
-    (void)hipFree(w.cnt);
-    w.ws = nullptr;
-  }
-  (void)hipGetLastError();  // a failed allocation leaves the data-parallel path in place, not an error
-  sk_map[key] = w;
-  return w.ws ? &sk_map[key] : nullptr;
-}
+size_t sk_part_bytes(int ctas) { return (size_t)2 * ctas * BM * BN * sizeof(float); }
 
 // KH_GEMM_TN192=0 keeps every data-parallel launch on 256-wide tiles (read per call)
 bool narrow_enabled() {
@@ -86,7 +58,7 @@ bool narrow_enabled() {
 // under 60 % of their last wave and 256-wide stream-K needs less work per CU (padded width x tiles / CUs
 // against waves x width).
 // tn_div > 0: the tile width must divide tn_div (sub-pixel convs: a tile may not straddle two phases).
-void plan_launch(GemmArgs& a, int epi, hipStream_t st, int& grid_x, int& tn, bool narrow128 = false, int tn_div = 0) {
+void plan_launch(GemmArgs& a, int epi, const GemmWs* ws, int& grid_x, int& tn, bool narrow128 = false, int tn_div = 0) {
   const int tiles_m = (a.M + BM - 1) / BM;
   const int nk = a.K / BK;
   auto padded = [&](int w) { return (a.N + w - 1) / w * w; };
@@ -118,11 +90,10 @@ void plan_launch(GemmArgs& a, int epi, hipStream_t st, int& grid_x, int& tn, boo
   if (sk_enabled() && tiles <= SK_MAX_TILES && (double)tiles / ((double)rounds * ctas) < 0.6) {
     const long long iters = (long long)tiles * nk;
     const int per = (int)((iters + ctas - 1) / ctas);
-    const SkWorkspace* w = per >= SK_MIN_ITERS ? sk_workspace(dev, st, ctas) : nullptr;
-    if (w) {
+    if (per >= SK_MIN_ITERS && ws && ws->p && ws->bytes >= gemm_workspace_bytes_for(ctas)) {
       a.sk_iters = per;
-      a.ws = w->ws;
-      a.cnt = w->cnt;
+      a.ws = (float*)ws->p;
+      a.cnt = (int*)((char*)ws->p + sk_part_bytes(ctas));
       grid_x = ctas;
       return;
     }
@@ -145,7 +116,7 @@ void plan_launch(GemmArgs& a, int epi, hipStream_t st, int& grid_x, int& tn, boo
 namespace {
 
 int gemm_run(hipStream_t st, int epi, const void* A, int a_dtype, const kh_weight& W, void* C, int M, int N, int K,
-             int lda, int ldw, int ldc, const void* vec, const QkNormRope* qk, Err& e) {
+             int lda, int ldw, int ldc, const void* vec, const QkNormRope* qk, const GemmWs* ws, Err& e) {
   if (epi < KH_EPI_STORE16 || epi > KH_EPI_BIAS_F32) return e.fail("gemm: unknown epilogue %d", epi);
   if (a_dtype != KH_F16 && a_dtype != KH_BF16) return e.fail("gemm: activations must be f16 or bf16");
   if (M <= 0 || N <= 0 || K <= 0) return e.fail("gemm: empty shape M=%d N=%d K=%d", M, N, K);
@@ -202,7 +173,8 @@ int gemm_run(hipStream_t st, int epi, const void* A, int a_dtype, const kh_weigh
     epi = EPI_QKNR;
   }
   int grid_x = 0, tn = BN;
-  plan_launch(a, epi, st, grid_x, tn, wf == WF_16);
+  if (ws && ws->p && ((uintptr_t)ws->p & 255)) return e.fail("gemm: workspace must be 256-byte aligned");
+  plan_launch(a, epi, ws, grid_x, tn, wf == WF_16);
   hipError_t r = a_dtype == KH_F16 ? launch_gemm_f16(wf, epi, a, grid_x, tn, st)
                                    : launch_gemm_bf16(wf, epi, a, grid_x, tn, st);
   if (r != hipSuccess) return e.hip(r, "gemm launch");
@@ -247,12 +219,40 @@ int pack_int8(hipStream_t st, const void* W, int K, int ldw, void* out, Err& e) 
 }
 
 int gemm(hipStream_t st, int epi, const void* A, int a_dtype, const kh_weight& W, void* C, int M, int N, int K,
-         int lda, int ldw, int ldc, const void* vec, Err& e) {
-  return gemm_run(st, epi, A, a_dtype, W, C, M, N, K, lda, ldw, ldc, vec, nullptr, e);
+         int lda, int ldw, int ldc, const void* vec, Err& e, const GemmWs* ws) {
+  return gemm_run(st, epi, A, a_dtype, W, C, M, N, K, lda, ldw, ldc, vec, nullptr, ws, e);
+}
+
+size_t gemm_workspace_bytes_for(int ctas) { return ctas > 0 ? sk_part_bytes(ctas) + SK_MAX_TILES * sizeof(int) : 0; }
+
+size_t gemm_workspace_bytes() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  return gemm_workspace_bytes_for(sk_cta_count(dev));
+}
+
+__global__ void zero_words_kernel(int* p, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+int gemm_workspace_init(hipStream_t st, void* ws, size_t bytes, Err& e) {
+  int dev = 0;
+  hipError_t r = hipGetDevice(&dev);
+  if (r != hipSuccess) return e.hip(r, "gemm_workspace_init: no device");
+  const int ctas = sk_cta_count(dev);
+  const size_t need = gemm_workspace_bytes_for(ctas);
+  if (!ws || bytes < need) return e.fail("gemm_workspace_init: workspace %zu bytes < %zu needed", bytes, need);
+  if ((uintptr_t)ws & 255) return e.fail("gemm_workspace_init: workspace must be 256-byte aligned");
+  // a kernel, not hipMemsetAsync, so the call can sit in a captured graph
+  hipLaunchKernelGGL(zero_words_kernel, dim3((SK_MAX_TILES + 255) / 256), dim3(256), 0, st,
+                     (int*)((char*)ws + sk_part_bytes(ctas)), SK_MAX_TILES);
+  r = hipGetLastError();
+  return r == hipSuccess ? KH_OK : e.hip(r, "gemm_workspace_init launch");
 }
 
 int gemm_qk_norm_rope(hipStream_t st, const void* A, int a_dtype, const kh_weight& W, void* C, int M, int N, int K,
-                      int lda, int ldw, int ldc, const QkNormRope& q, Err& e) {
+                      int lda, int ldw, int ldc, const QkNormRope& q, Err& e, const GemmWs* ws) {
   if (q.mode < 0 || q.mode > 2) return e.fail("gemm_qk_norm_rope: bad rope mode %d", q.mode);
   if (q.mode != 2 && (!q.cosb || !q.sinb)) return e.fail("gemm_qk_norm_rope: rope needs cos / sin tables");
   if (q.n_q < 0 || q.n_k < 0 || q.n_q + q.n_k == 0) return e.fail("gemm_qk_norm_rope: no q / k heads");
@@ -265,7 +265,7 @@ int gemm_qk_norm_rope(hipStream_t st, const void* A, int a_dtype, const kh_weigh
     return e.fail("gemm_qk_norm_rope: big_dim needs qbig / kbig");
   if (((uintptr_t)q.wq | (uintptr_t)q.wk | (uintptr_t)q.cosb | (uintptr_t)q.sinb) & 15)
     return e.fail("gemm_qk_norm_rope: norm weights and tables must be 16-byte aligned");
-  return gemm_run(st, KH_EPI_STORE16, A, a_dtype, W, C, M, N, K, lda, ldw, ldc, nullptr, &q, e);
+  return gemm_run(st, KH_EPI_STORE16, A, a_dtype, W, C, M, N, K, lda, ldw, ldc, nullptr, &q, ws, e);
 }
 
 }  // namespace kh
@@ -273,7 +273,7 @@ int gemm_qk_norm_rope(hipStream_t st, const void* A, int a_dtype, const kh_weigh
 namespace kh {
 
 int conv3x3(hipStream_t st, const void* x, int ldx, int C, int H, int W, int up, int dtype, const kh_weight& Wt, int K,
-            int N, const float* bias, const void* res, void* y, int ldy, Err& e) {
+            int N, const float* bias, const void* res, void* y, int ldy, Err& e, const GemmWs* ws) {
   if (dtype != KH_F16 && dtype != KH_BF16) return e.fail("conv3x3: dtype must be f16 or bf16");
   if (!x || !Wt.w || !y || !bias) return e.fail("conv3x3: null x / W / bias / y");
   if (Wt.w_dtype != dtype) return e.fail("conv3x3: weights must be 16-bit of the activation type");
@@ -290,7 +290,8 @@ int conv3x3(hipStream_t st, const void* x, int ldx, int C, int H, int W, int up,
   GemmArgs a{x, Wt.w, nullptr, y, bias, H * W, N, K, ldx, N, ldy, 0, KH_F32, 0, nullptr, nullptr,
              C, H, W, up ? 1 : 0, (uint32_t)((((uint64_t)1 << 32) + (uint64_t)C - 1) / (uint64_t)C), res, ldy};
   int grid_x = 0, tn = BN;
-  plan_launch(a, KH_EPI_BIAS16, st, grid_x, tn, true);
+  if (ws && ws->p && ((uintptr_t)ws->p & 255)) return e.fail("conv3x3: workspace must be 256-byte aligned");
+  plan_launch(a, KH_EPI_BIAS16, ws, grid_x, tn, true);
   const hipError_t r = dtype == KH_F16 ? launch_conv_f16(a, grid_x, tn, st) : launch_conv_bf16(a, grid_x, tn, st);
   if (r != hipSuccess) return e.hip(r, "conv3x3 launch");
   return KH_OK;
@@ -302,7 +303,7 @@ int conv3x3(hipStream_t st, const void* x, int ldx, int C, int H, int W, int up,
 namespace kh {
 
 int conv_up2_subpix(hipStream_t st, const void* x, int ldx, int C, int H, int W, int dtype, const kh_weight& W2, int K,
-                    int Np, const float* bias4, void* y, int ldy, Err& e) {
+                    int Np, const float* bias4, void* y, int ldy, Err& e, const GemmWs* ws) {
   if (dtype != KH_F16 && dtype != KH_BF16) return e.fail("conv_up2: dtype must be f16 or bf16");
   if (!x || !W2.w || !y || !bias4) return e.fail("conv_up2: null x / W2 / bias / y");
   if (W2.w_dtype != dtype) return e.fail("conv_up2: weights must be 16-bit of the activation type");
@@ -320,7 +321,8 @@ int conv_up2_subpix(hipStream_t st, const void* x, int ldx, int C, int H, int W,
   a.cv_np = Np;
   a.cv_winv = (uint32_t)((((uint64_t)1 << 32) + (uint64_t)W - 1) / (uint64_t)W);
   int grid_x = 0, tn = BN;
-  plan_launch(a, KH_EPI_BIAS16, st, grid_x, tn, true, Np);
+  if (ws && ws->p && ((uintptr_t)ws->p & 255)) return e.fail("conv_up2: workspace must be 256-byte aligned");
+  plan_launch(a, KH_EPI_BIAS16, ws, grid_x, tn, true, Np);
   const hipError_t r = dtype == KH_F16 ? launch_conv_f16(a, grid_x, tn, st) : launch_conv_bf16(a, grid_x, tn, st);
   if (r != hipSuccess) return e.hip(r, "conv_up2 launch");
   return KH_OK;

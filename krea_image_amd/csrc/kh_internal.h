@@ -32,9 +32,19 @@ struct Err {
   }
 };
 
+// Stream-K workspace of a GEMM launch (caller-owned device memory, 256-byte aligned, its counter words zeroed once
+// by gemm_workspace_init); a launch without one (or with one too small) runs data-parallel.
+struct GemmWs {
+  void* p;
+  size_t bytes;
+};
+size_t gemm_workspace_bytes_for(int ctas);
+size_t gemm_workspace_bytes();  // for the current device
+int gemm_workspace_init(hipStream_t st, void* ws, size_t bytes, Err& e);
+
 int pack_int8(hipStream_t st, const void* W, int K, int ldw, void* out, Err& e);
 int gemm(hipStream_t st, int epi, const void* A, int a_dtype, const kh_weight& W, void* C, int M, int N, int K,
-         int lda, int ldw, int ldc, const void* vec, Err& e);
+         int lda, int ldw, int ldc, const void* vec, Err& e, const GemmWs* ws = nullptr);
 // the per-head RMSNorm + RoPE of qk_norm_rope fused into a STORE16 GEMM's epilogue
 struct QkNormRope {
   const float *wq, *wk, *cosb, *sinb;
@@ -43,13 +53,13 @@ struct QkNormRope {
   float eps;
 };
 int gemm_qk_norm_rope(hipStream_t st, const void* A, int a_dtype, const kh_weight& W, void* C, int M, int N, int K,
-                      int lda, int ldw, int ldc, const QkNormRope& q, Err& e);
+                      int lda, int ldw, int ldc, const QkNormRope& q, Err& e, const GemmWs* ws = nullptr);
 int conv_up2_subpix(hipStream_t st, const void* x, int ldx, int C, int H, int W, int dtype, const kh_weight& W2, int K,
-                    int Np, const float* bias4, void* y, int ldy, Err& e);
+                    int Np, const float* bias4, void* y, int ldy, Err& e, const GemmWs* ws = nullptr);
 int vae_subpix_weights(hipStream_t st, const void* w, int dtype, int Cin, int Cout, void* w2, int Kp, int Np,
                        const float* b, float* b4, Err& e);
 int conv3x3(hipStream_t st, const void* x, int ldx, int C, int H, int W, int up, int dtype, const kh_weight& Wt, int K,
-            int N, const float* bias, const void* res, void* y, int ldy, Err& e);
+            int N, const float* bias, const void* res, void* y, int ldy, Err& e, const GemmWs* ws = nullptr);
 
 int attention(hipStream_t st, const void* Q, const void* K, const void* V, void* O, int dtype, int Lq, int Lk,
               int heads, int ldq, int ldk, int ldv, int ldo, int group, int causal, int q_pos0, const void* G,
@@ -64,6 +74,11 @@ int gemv(hipStream_t st, const float* x, const kh_weight& W, float* y, int rows,
          const float* bias, Err& e);
 int make_cond(hipStream_t st, const float* tvec, const float* table, const float* n1, const float* n2, int D,
               float* mods, Err& e);
+int make_fin(hipStream_t st, const float* t, const float* lin, const float* nf, int D, float* fin, Err& e);
+// copies n <= 256 host floats to dst by a kernel argument (stream-ordered, no staging buffer)
+int store_vec(hipStream_t st, const float* host, int n, float* dst, Err& e);
+int conditioning(hipStream_t st, const kh_qw* f, int fast, float sigma, float* t, float* tvec, float* work,
+                 size_t work_bytes, int* from_table, Err& e);
 int gemm_f32(hipStream_t st, const float* A, const float* W, float* C, int M, int N, int K, int lda, int ldw, int ldc,
              int mode, const float* bias, Err& e);
 int dit_layer_forward(hipStream_t st, const kh_dit_config& c, const kh_dit_layer& L, const kh_dit_state& s, int R,

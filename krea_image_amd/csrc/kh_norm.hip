@@ -168,67 +168,79 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(uint16_t* __restrict_
 }
 
 // ------------------------------------------------------------------------------------------------------
-// adaLN modulation GEMV: y[r, n] (+)= sum_k act(x[r, k]) W~[k, n] (+ bias[n]), rows <= 4, x / y f32.
-// engine/kernels/gemm.metal:346-371 (gemv_bf16: act bit 0 = SiLU on load, bit 1 = accumulate) with the
-// weight formats of kh_gemm. HBM-bound (each weight byte is read once): grid (N / COLS, KSPLIT); a lane owns
-// 16 consecutive bytes of a weight row (16 int8 columns, or 8 16-bit ones), so a wave reads 1 KB per row;
-// the 4 waves split the slab's rows, each keeping 8 rows' loads in flight, reduce through LDS and add into y
-// with one f32 atomic per column. y is initialised (bias, or 0, or kept for accumulation) by gemv_init.
-constexpr int GEMV_KSPLIT_MAX = 64;
+// adaLN / conditioning GEMV: y[r, n] = (y[r, n] if accumulate) + bias[n] + sum_k act(x[r, k]) W~[k, n],
+// rows <= 4, x / y f32. engine/kernels/gemm.metal:346-371 (gemv_bf16: act bit 0 = SiLU on load, bit 1 =
+// accumulate) and the f32 cblas_sgemv linears of Conditioning::compute (engine/src/model.mm:582-590: the GELU
+// between them is applied on load, act bit 2), with the weight formats of kh_gemm plus f32.
+// HBM-bound, every weight byte is read once. A workgroup owns a 32-byte column slab of every weight row (32
+// int8 / 16 16-bit / 8 f32 columns) over all of K: two lanes of 16 bytes per row, 128 k-groups of contiguous
+// rows, 8 rows' loads in flight per lane. The k-groups' partial sums are added through LDS in a fixed order
+// (no atomics, no second launch): the same inputs give the same bits on every run. The four slabs of one
+// 128-byte line go to workgroups on the same XCD (the dispatcher deals workgroups round-robin to the 8 XCDs,
+// each with its own L2), so a line is fetched from HBM once.
+constexpr int GEMV_KG = 128;  // k-groups per workgroup (two lanes each)
 
-__global__ void gemv_init(float* y, const float* bias, int rows, int N, int ldy, int accumulate) {
-  const int n = blockIdx.x * blockDim.x + threadIdx.x;
-  if (n >= N) return;
-  for (int r = 0; r < rows; r++) {
-    const float b = bias ? bias[n] : 0.f;
-    float* yp = y + (size_t)r * ldy + n;
-    *yp = accumulate ? *yp + b : b;
-  }
+template <int ACT>
+__device__ __forceinline__ float gemv_act(float v) {
+  if (ACT == 1) return silu_f(v);
+  if (ACT == 4) return gelu_tanh_f(v);
+  return v;
 }
 
-// WF 0: 16-bit weights (8 columns per lane), 1: int8 per-channel, 2: int8 group (16 per lane); RMAX: rows the
-// instantiation handles (1: the DiT's single conditioning vector, 4: up to four; sizes the accumulators and the
-// partial-sum LDS, so the one-row form fits four times as many workgroups per CU)
-template <int WF, int RMAX>
+// WF 0: 16-bit weights, 1: int8 per-channel scales, 2: int8 group scales, 3: f32. RMAX: rows the instantiation
+// handles (sizes the accumulators and the LDS; the one-row form fits four times as many workgroups per CU).
+template <int WF, int RMAX, int ACT>
 __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, const void* __restrict__ W,
                                                    const void* __restrict__ S, int s_dtype, int group, int w16_dtype,
-                                                   float* __restrict__ y, int rows, int N, int K, int ldw, int ldy,
-                                                   int silu, int kchunk) {
-  constexpr int CPL = WF == 0 ? 8 : 16;  // columns per lane
-  constexpr int COLS = 16 * CPL;         // 16 lanes span the block's columns; lane >> 4 picks a row group
-  __shared__ float xs[RMAX][512];        // activated x of this slab (rows x kchunk), kchunk <= 512
-  __shared__ float part[16][RMAX][COLS]; // [row group][row][column]
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int rg = wave * 4 + (lane >> 4);  // 16 row groups
-  const int n = blockIdx.x * COLS + (lane & 15) * CPL;
-  const int k0 = blockIdx.y * kchunk, k1 = min(K, k0 + kchunk);
-  for (int i = tid; i < rows * (k1 - k0); i += 256) {
-    const int r = i / (k1 - k0), k = i % (k1 - k0);
-    const float v = x[(size_t)r * K + k0 + k];
-    xs[r][k] = silu ? silu_f(v) : v;
-  }
-  __syncthreads();
+                                                   const float* __restrict__ bias, float* __restrict__ y, int rows,
+                                                   int N, int K, int ldw, int accumulate) {
+  constexpr int ES = WF == 3 ? 4 : WF == 0 ? 2 : 1;  // bytes per weight
+  constexpr int CPL = 16 / ES;                        // columns per lane
+  constexpr int COLS = 2 * CPL;                       // columns per workgroup
+  constexpr int OUT = RMAX * COLS;                    // partial sums per k-group
+  constexpr int TPO = 256 / OUT;                      // threads per output in the final reduction
+  __shared__ float part[GEMV_KG][OUT + 1];
+  const int tid = threadIdx.x, li = tid & 1, kg = tid >> 1;
+  const int nblk = gridDim.x;
+  const int b = nblk % 8 == 0 ? (int)(blockIdx.x & 7) * (nblk >> 3) + (int)(blockIdx.x >> 3) : (int)blockIdx.x;
+  const int n0 = b * COLS, n = n0 + li * CPL;
+  const int kr = (K + GEMV_KG - 1) / GEMV_KG;
+  const int k0 = min(K, kg * kr), k1 = min(K, k0 + kr);
   float acc[RMAX][CPL];
 #pragma unroll
   for (int r = 0; r < RMAX; r++)
 #pragma unroll
     for (int c = 0; c < CPL; c++) acc[r][c] = 0.f;
   if (n < N) {
-    const char* wp = (const char*)W + ((size_t)n) * (WF == 0 ? 2 : 1);
-    const size_t row_bytes = (size_t)ldw * (WF == 0 ? 2 : 1);
-    for (int kb = k0 + rg; kb < k1; kb += 16 * 8) {
+    const char* wp = (const char*)W + (size_t)n * ES;
+    const size_t rb = (size_t)ldw * ES;
+    int gcur = -1;
+    float sc[CPL];
+    for (int kb = k0; kb < k1; kb += 8) {
       u32x4 raw[8];
 #pragma unroll
       for (int u = 0; u < 8; u++) {
-        const int k = kb + 16 * u;
-        raw[u] = k < k1 ? *(const u32x4*)(wp + (size_t)k * row_bytes) : (u32x4){0u, 0u, 0u, 0u};
+        const int k = kb + u;
+        raw[u] = k < k1 ? *(const u32x4*)(wp + (size_t)k * rb) : (u32x4){0u, 0u, 0u, 0u};
       }
+      float xa[RMAX][8];  // activated inputs of these 8 rows (loaded while the weights are in flight)
+#pragma unroll
+      for (int r = 0; r < RMAX; r++)
+#pragma unroll
+        for (int u = 0; u < 8; u++) xa[r][u] = (r < rows && kb + u < k1) ? x[(size_t)r * K + kb + u] : 0.f;
+#pragma unroll
+      for (int r = 0; r < RMAX; r++)
+#pragma unroll
+        for (int u = 0; u < 8; u++) xa[r][u] = gemv_act<ACT>(xa[r][u]);
 #pragma unroll
       for (int u = 0; u < 8; u++) {
-        const int k = kb + 16 * u;
+        const int k = kb + u;
         if (k >= k1) break;
         float wv[CPL];
-        if (WF == 0) {
+        if (WF == 3) {
+#pragma unroll
+          for (int c = 0; c < 4; c++) wv[c] = __builtin_bit_cast(float, raw[u][c]);
+        } else if (WF == 0) {
 #pragma unroll
           for (int c = 0; c < 8; c++) {
             const uint16_t hb = (uint16_t)(raw[u][c >> 1] >> (16 * (c & 1)));
@@ -238,15 +250,20 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
 #pragma unroll
           for (int c = 0; c < 16; c++) wv[c] = (float)(int8_t)(raw[u][c >> 2] >> (8 * (c & 3)));
           if (WF == 2) {
-            const size_t g = (size_t)(k / group) * ldw + n;
+            const int g = k / group;
+            if (g != gcur) {
+              gcur = g;
 #pragma unroll
-            for (int c = 0; c < 16; c++) wv[c] *= load_scale(S, s_dtype, g + c);
+              for (int c = 0; c < 16; c++) sc[c] = load_scale(S, s_dtype, (size_t)g * ldw + n + c);
+            }
+#pragma unroll
+            for (int c = 0; c < 16; c++) wv[c] *= sc[c];
           }
         }
 #pragma unroll
         for (int r = 0; r < RMAX; r++) {  // static indices keep acc in registers
           if (r >= rows) break;
-          const float xv = xs[r][k - k0];
+          const float xv = xa[r][u];
 #pragma unroll
           for (int c = 0; c < CPL; c++) acc[r][c] += xv * wv[c];
         }
@@ -254,21 +271,24 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
     }
   }
 #pragma unroll
-  for (int r = 0; r < RMAX; r++) {
-    if (r >= rows) break;
+  for (int r = 0; r < RMAX; r++)
 #pragma unroll
-    for (int c = 0; c < CPL; c++) part[rg][r][(lane & 15) * CPL + c] = acc[r][c];
-  }
+    for (int c = 0; c < CPL; c++) part[kg][r * COLS + li * CPL + c] = acc[r][c];
   __syncthreads();
-  for (int i = tid; i < rows * COLS; i += 256) {
-    const int r = i / COLS, c = i % COLS;
-    const int nc = blockIdx.x * COLS + c;
-    if (nc >= N) continue;
-    float v = 0.f;
+  // output o = (row, column) summed by TPO adjacent lanes, each over GEMV_KG / TPO k-groups in order, then a
+  // fixed butterfly over those lanes
+  const int o = tid / TPO, j = tid % TPO;
+  float v = 0.f;
+#pragma unroll 4
+  for (int i = 0; i < GEMV_KG / TPO; i++) v += part[j * (GEMV_KG / TPO) + i][o];
 #pragma unroll
-    for (int g = 0; g < 16; g++) v += part[g][r][c];
+  for (int m = TPO / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+  const int r = o / COLS, nc = n0 + o % COLS;
+  if (j == 0 && r < rows && nc < N) {
     if (WF == 1) v *= load_scale(S, s_dtype, nc);
-    atomicAdd(y + (size_t)r * ldy + nc, v);
+    const float bv = bias ? bias[nc] : 0.f;
+    float* yp = y + (size_t)r * N + nc;
+    *yp = (accumulate ? *yp + bv : bv) + v;
   }
 }
 
@@ -290,56 +310,68 @@ __global__ void make_cond_kernel(const float* tvec, const float* table, const fl
   mods[5 * D + k] = v[5];
 }
 
-// ------------------------------------------------------------------------------------------------------
-// fp32 GEMM of the patch embed (64 -> D) and the final projection (D -> 64): engine/kernels/f32gemm.metal
-// (gemm_f32w) with its modes bit 0 bias, bit 1 GELU(tanh), bit 2 accumulate. 64 x 64 tiles, 256 threads,
-// 4 x 4 outputs per thread, K staged 16 at a time through LDS. Tiny next to the DiT layers.
-// Split-K form (gridDim.z > 1, no GELU): each z-slice adds its partial product into C with f32 atomics after
-// gemm_f32_init has set C to bias / 0 (or kept it, for accumulate).
-__global__ void gemm_f32_init(float* C, const float* bias, int M, int N, int ldc, int mode) {
-  const int n = blockIdx.x * blockDim.x + threadIdx.x, m = blockIdx.y;
-  if (n >= N) return;
-  float* cp = C + (size_t)m * ldc + n;
-  const float b = (mode & 1) ? bias[n] : 0.f;
-  *cp = (mode & 4) ? *cp + b : b;
+// Final-norm vectors of the head from the step's t: engine/src/model.mm:340-346 (the fin half of
+// DiT::make_cond): fin[k] = nf[k] (1 + t[k] + lin[k]), fin[D + k] = t[k] + lin[D + k].
+__global__ void make_fin_kernel(const float* t, const float* lin, const float* nf, int D, float* fin) {
+  const int k = blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= D) return;
+  fin[k] = nf[k] * (1.0f + t[k] + lin[k]);
+  fin[D + k] = t[k] + lin[D + k];
 }
 
+// A host-computed vector of up to 256 floats passed by value (the timestep embedding of Conditioning::compute)
+struct Vec256 {
+  float v[256];
+};
+__global__ void store_vec_kernel(Vec256 src, int n, float* dst) {
+  const int i = threadIdx.x;
+  if (i < n) dst[i] = src.v[i];
+}
+
+// ------------------------------------------------------------------------------------------------------
+// fp32 GEMM of the patch embed (64 -> D) and the final projection (D -> 64): engine/kernels/f32gemm.metal
+// (gemm_f32w) with its modes bit 0 bias, bit 1 GELU(tanh), bit 2 accumulate. Tiles of 16 TM rows x 64 columns,
+// 256 threads, TM x 4 outputs per thread, K staged 16 at a time through LDS, each output summed over all of K
+// in order by one thread (no split-K atomics: the results repeat bit for bit). TM = 4 (64-row tiles) unless
+// that leaves CUs idle (the D -> 64 head: 64 tiles at 4096 rows), then TM = 1. Tiny next to the DiT layers.
+template <int TM>
 __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ W,
                                                        float* __restrict__ C, const float* __restrict__ bias, int M,
                                                        int N, int K, int lda, int ldw, int ldc, int mode) {
-  const int kz = gridDim.z > 1 ? (K + gridDim.z - 1) / gridDim.z : K;
-  const int kbeg = blockIdx.z * kz, kfin = min(K, kbeg + kz);
-  __shared__ float As[16][64 + 1];
+  constexpr int BMR = 16 * TM;
+  __shared__ float As[16][BMR + 1];
   __shared__ float Ws[16][64];
   const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
-  const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
-  float acc[4][4] = {};
-  for (int k0 = kbeg; k0 < kfin; k0 += 16) {
-    for (int i = tid; i < 16 * 64; i += 256) {
-      const int r = i / 16, c = i % 16;  // A tile: 64 rows x 16 k
+  const int m0 = blockIdx.y * BMR, n0 = blockIdx.x * 64;
+  float acc[TM][4] = {};
+  for (int k0 = 0; k0 < K; k0 += 16) {
+    for (int i = tid; i < 16 * BMR; i += 256) {
+      const int r = i / 16, c = i % 16;  // A tile: BMR rows x 16 k
       const int m = m0 + r, k = k0 + c;
-      As[c][r] = (m < M && k < kfin) ? A[(size_t)m * lda + k] : 0.f;
+      As[c][r] = (m < M && k < K) ? A[(size_t)m * lda + k] : 0.f;
+    }
+    for (int i = tid; i < 16 * 64; i += 256) {
       const int kr = i / 64, nc = i % 64;  // W tile: 16 k x 64 cols
-      Ws[kr][nc] = (k0 + kr < kfin && n0 + nc < N) ? W[(size_t)(k0 + kr) * ldw + n0 + nc] : 0.f;
+      Ws[kr][nc] = (k0 + kr < K && n0 + nc < N) ? W[(size_t)(k0 + kr) * ldw + n0 + nc] : 0.f;
     }
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < 16; k++) {
-      float a[4], b[4];
+      float a[TM], b[4];
 #pragma unroll
-      for (int i = 0; i < 4; i++) a[i] = As[k][ty * 4 + i];
+      for (int i = 0; i < TM; i++) a[i] = As[k][ty * TM + i];
 #pragma unroll
       for (int j = 0; j < 4; j++) b[j] = Ws[k][tx * 4 + j];
 #pragma unroll
-      for (int i = 0; i < 4; i++)
+      for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] += a[i] * b[j];
     }
     __syncthreads();
   }
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int m = m0 + ty * 4 + i;
+  for (int i = 0; i < TM; i++) {
+    const int m = m0 + ty * TM + i;
     if (m >= M) continue;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
@@ -347,10 +379,6 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
       if (n >= N) continue;
       float v = acc[i][j];
       float* cp = C + (size_t)m * ldc + n;
-      if (gridDim.z > 1) {
-        atomicAdd(cp, v);
-        continue;
-      }
       if (mode & 1) v += bias[n];
       if (mode & 2) v = gelu_tanh_f(v);
       *cp = (mode & 4) ? *cp + v : v;
@@ -416,43 +444,59 @@ int gemv(hipStream_t st, const float* x, const kh_weight& W, float* y, int rows,
   if (rows <= 0 || rows > 4 || N <= 0 || K <= 0) return e.fail("gemv: rows must be 1..4 and N, K > 0");
   if (ldw < N) return e.fail("gemv: ldw %d < N %d", ldw, N);
   if (!x || !W.w || !y) return e.fail("gemv: null x / W / y");
+  if (act & ~7) return e.fail("gemv: unknown act bits 0x%x", act);
+  if ((act & 1) && (act & 4)) return e.fail("gemv: SiLU and GELU on load are exclusive");
   int wf, group = K;
   if (W.w_dtype == KH_I8) {
     if (!W.s) return e.fail("gemv: int8 weights need scales");
+    if (W.s_dtype != KH_F32 && W.s_dtype != KH_F16 && W.s_dtype != KH_BF16) return e.fail("gemv: bad scale dtype");
     group = W.group <= 0 ? K : W.group;
     if (group > K || K % group) return e.fail("gemv: bad group %d", group);
     wf = group == K ? 1 : 2;
   } else if (W.w_dtype == KH_F16 || W.w_dtype == KH_BF16) {
     wf = 0;
+  } else if (W.w_dtype == KH_F32) {
+    wf = 3;
   } else {
     return e.fail(W.w_dtype == KH_I8P ? "gemv: packed int8 weights (KH_I8P) are for kh_gemm; pass the KH_I8 layout"
-                                      : "gemv: weight dtype must be int8, f16 or bf16");
+                                      : "gemv: weight dtype must be int8, f16, bf16 or f32");
   }
-  // K split so the grid has >= wg_target workgroups; each slab's x fits the 512-entry LDS stage
-  const int cols = wf == 0 ? 128 : 256;
-  if (N % (wf == 0 ? 8 : 16) || ldw % 16) return e.fail("gemv: N must be a multiple of 16 (8 for 16-bit), ldw of 16");
-  const int col_blocks = (N + cols - 1) / cols;
-  int ksplit = 1;
-  // one-row calls fit six workgroups per CU: more K splits keep more loads in flight (measured at 3072 ->
-  // 18432 int8: 512 workgroups 15.1 us, 1024 13.8 us, 2048 14.5 us)
-  const int wg_target = rows == 1 ? 1024 : 512;
-  while (ksplit < GEMV_KSPLIT_MAX && (col_blocks * ksplit < wg_target || (K + ksplit - 1) / ksplit > 512)) ksplit *= 2;
-  const int kchunk = (K + ksplit - 1) / ksplit;
-  if (kchunk > 512) return e.fail("gemv: K %d too large", K);
-  hipLaunchKernelGGL(gemv_init, dim3((N + 255) / 256), dim3(256), 0, st, y, bias, rows, N, N, (act & 2) ? 1 : 0);
-  dim3 grid(col_blocks, (K + kchunk - 1) / kchunk), block(256);
-#define KH_GEMV(WF_, R_)                                                                                      \
-  hipLaunchKernelGGL((gemv_kernel<WF_, R_>), grid, block, 0, st, x, W.w, W.s, W.s_dtype, group, W.w_dtype, y, rows, \
-                     N, K, ldw, N, act & 1, kchunk)
-  if (rows == 1) {
-    if (wf == 0) KH_GEMV(0, 1);
-    else if (wf == 1) KH_GEMV(1, 1);
-    else KH_GEMV(2, 1);
-  } else {
-    if (wf == 0) KH_GEMV(0, 4);
-    else if (wf == 1) KH_GEMV(1, 4);
-    else KH_GEMV(2, 4);
-  }
+  const int es = wf == 3 ? 4 : wf == 0 ? 2 : 1, cpl = 16 / es;
+  if (N % cpl || ((size_t)ldw * es) % 16)
+    return e.fail("gemv: N must be a multiple of %d and weight rows 16-byte aligned for this weight type", cpl);
+  if (((uintptr_t)W.w & 15)) return e.fail("gemv: W must be 16-byte aligned");
+  dim3 grid((unsigned)((N + 2 * cpl - 1) / (2 * cpl))), block(256);
+  const int accumulate = (act & 2) ? 1 : 0;
+  const int a = act & 5;
+#define KH_GEMV(WF_, R_, A_)                                                                                   \
+  hipLaunchKernelGGL((gemv_kernel<WF_, R_, A_>), grid, block, 0, st, x, W.w, W.s, W.s_dtype, group, W.w_dtype, \
+                     bias, y, rows, N, K, ldw, accumulate)
+#define KH_GEMV_A(WF_, R_) \
+  do {                     \
+    if (a == 1)            \
+      KH_GEMV(WF_, R_, 1); \
+    else if (a == 4)       \
+      KH_GEMV(WF_, R_, 4); \
+    else                   \
+      KH_GEMV(WF_, R_, 0); \
+  } while (0)
+#define KH_GEMV_W(R_)     \
+  do {                    \
+    if (wf == 0)          \
+      KH_GEMV_A(0, R_);   \
+    else if (wf == 1)     \
+      KH_GEMV_A(1, R_);   \
+    else if (wf == 2)     \
+      KH_GEMV_A(2, R_);   \
+    else                  \
+      KH_GEMV_A(3, R_);   \
+  } while (0)
+  if (rows == 1)
+    KH_GEMV_W(1);
+  else
+    KH_GEMV_W(4);
+#undef KH_GEMV_W
+#undef KH_GEMV_A
 #undef KH_GEMV
   const hipError_t r = hipGetLastError();
   return r == hipSuccess ? KH_OK : e.hip(r, "gemv launch");
@@ -512,16 +556,31 @@ int gemm_f32(hipStream_t st, const float* A, const float* W, float* C, int M, in
   if (M <= 0 || N <= 0 || K <= 0) return e.fail("gemm_f32: empty shape");
   if (!A || !W || !C || ((mode & 1) && !bias)) return e.fail("gemm_f32: null A / W / C (or bias for mode & 1)");
   if (lda < K || ldw < N || ldc < N) return e.fail("gemm_f32: bad strides");
-  dim3 grid((N + 63) / 64, (M + 63) / 64), block(256);
-  // small grids with long K (the D -> 64 head) split K over workgroups; GELU needs the full sum
-  int ksplit = 1;
-  while (!(mode & 2) && grid.x * grid.y * ksplit < 512 && K / (ksplit * 2) >= 128) ksplit *= 2;
-  grid.z = ksplit;
-  if (ksplit > 1)
-    hipLaunchKernelGGL(gemm_f32_init, dim3((N + 255) / 256, M), dim3(256), 0, st, C, bias, M, N, ldc, mode);
-  hipLaunchKernelGGL(gemm_f32_kernel, grid, block, 0, st, A, W, C, bias, M, N, K, lda, ldw, ldc, mode);
+  const unsigned gx = (unsigned)((N + 63) / 64);
+  if ((size_t)gx * ((M + 63) / 64) >= 256)
+    hipLaunchKernelGGL(gemm_f32_kernel<4>, dim3(gx, (M + 63) / 64), dim3(256), 0, st, A, W, C, bias, M, N, K, lda, ldw,
+                       ldc, mode);
+  else
+    hipLaunchKernelGGL(gemm_f32_kernel<1>, dim3(gx, (M + 15) / 16), dim3(256), 0, st, A, W, C, bias, M, N, K, lda, ldw,
+                       ldc, mode);
   const hipError_t r = hipGetLastError();
   return r == hipSuccess ? KH_OK : e.hip(r, "gemm_f32 launch");
+}
+
+int make_fin(hipStream_t st, const float* t, const float* lin, const float* nf, int D, float* fin, Err& e) {
+  if (D <= 0 || !t || !lin || !nf || !fin) return e.fail("make_fin: null vector or D <= 0");
+  hipLaunchKernelGGL(make_fin_kernel, dim3((D + 255) / 256), dim3(256), 0, st, t, lin, nf, D, fin);
+  const hipError_t r = hipGetLastError();
+  return r == hipSuccess ? KH_OK : e.hip(r, "make_fin launch");
+}
+
+int store_vec(hipStream_t st, const float* host, int n, float* dst, Err& e) {
+  if (n <= 0 || n > 256 || !host || !dst) return e.fail("store_vec: 1..256 values");
+  Vec256 v{};
+  for (int i = 0; i < n; i++) v.v[i] = host[i];
+  hipLaunchKernelGGL(store_vec_kernel, dim3(1), dim3(256), 0, st, v, n, dst);
+  const hipError_t r = hipGetLastError();
+  return r == hipSuccess ? KH_OK : e.hip(r, "store_vec launch");
 }
 
 }  // namespace kh

@@ -1,9 +1,9 @@
 // VAE decoder host loop (engine/src/vae.mm:289-337, VAEDecoder::run) over libkh ops: latent unpack ->
 // conv_in -> mid (resblock, attention, resblock) -> 4 up blocks (3 resblocks each, nearest-2x + 3x3 upsampler
 // after the first three) -> RMS norm + SiLU -> conv_out -> RGBA8. Weights are read by name from an uploaded
-// .qw file (the converter's vae.qw layout, tools/convert.py:347-390). Every buffer comes from the caller's
-// workspace (kh_vae_workspace_bytes), apart from the GEMM's stream-K partials (allocated once per stream);
-// everything is enqueued on one stream.
+// .qw file (the converter's vae.qw layout, tools/convert.py:347-390). Every buffer, the GEMMs' stream-K
+// workspace included, comes from the caller's workspace (kh_vae_workspace_bytes); everything is enqueued on one
+// stream.
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
@@ -36,8 +36,8 @@ long long query_chunk(long long P0, long long Pp0) {
 
 struct Plan {
   long long P0, P3, Pp0, qc;  // VAE-input pixels, output pixels, P0 rounded up to 64, attention query chunk
-  size_t act, wpad, bpad, qkv, kt, S, Pm, total;
-  size_t off_act[5], off_wpad, off_bpad, off_qkv, off_kt, off_S, off_Pm;
+  size_t act, wpad, bpad, qkv, kt, S, Pm, gws, total;
+  size_t off_act[5], off_wpad, off_bpad, off_qkv, off_kt, off_S, off_Pm, off_gws;
 };
 
 Plan plan(int H16, int W16) {
@@ -67,6 +67,8 @@ Plan plan(int H16, int W16) {
   p.off_kt = off, off += p.kt;
   p.off_S = off, off += p.S;
   p.off_Pm = off, off += p.Pm;
+  p.gws = (size_t)ru((long long)gemm_workspace_bytes(), 256);
+  p.off_gws = off, off += p.gws;
   p.total = off;
   return p;
 }
@@ -80,7 +82,8 @@ struct Act {
 
 class Decoder {
  public:
-  Decoder(hipStream_t st, const kh_qw* f, const Plan& pl, char* ws, Err& e) : st_(st), f_(f), pl_(pl), ws_(ws), e_(e) {}
+  Decoder(hipStream_t st, const kh_qw* f, const Plan& pl, char* ws, Err& e)
+      : st_(st), f_(f), pl_(pl), ws_(ws), e_(e), gws_{ws + pl.off_gws, pl.gws} {}
 
   int run(const float* z, int H16, int W16, void* rgba);
 
@@ -90,6 +93,7 @@ class Decoder {
   const Plan& pl_;
   char* ws_;
   Err& e_;
+  const GemmWs gws_;  // the GEMMs' stream-K workspace, inside ws_
   bool used_[5] = {false, false, false, false, false};
 
   int acquire(int H, int W, int C, int ld, Act& a) {
@@ -144,7 +148,7 @@ class Decoder {
       if (res) return e_.fail("vae: no residual on an upsampling conv");
       if ((rc = acquire(2 * x.H, 2 * x.W, cout, Np, y))) return rc;
       const kh_weight w2{wp, nullptr, KH_BF16, KH_F32, 0};
-      return conv_up2_subpix(st_, x.p, x.ld, x.C, x.H, x.W, KH_BF16, w2, K2, Np, bp, y.p, Np, e_);
+      return conv_up2_subpix(st_, x.p, x.ld, x.C, x.H, x.W, KH_BF16, w2, K2, Np, bp, y.p, Np, e_, &gws_);
     }
     if (Kp != K || Np != cout) {  // the GEMM's K and N multiples of 64: zero rows / columns
       uint16_t* wp = (uint16_t*)(ws_ + pl_.off_wpad);
@@ -159,7 +163,7 @@ class Decoder {
     const kh_weight wt{W, nullptr, KH_BF16, KH_F32, 0};
     if (res && (res->ld != y.ld || res->P() != y.P())) return e_.fail("vae: residual shape mismatch");
     // the residual add is fused into the GEMM epilogue (the reference's vconv res input, vae.mm:112-125)
-    return kh::conv3x3(st_, x.p, x.ld, x.C, H, Wd, up, KH_BF16, wt, Kp, Np, bias, res ? res->p : nullptr, y.p, Np, e_);
+    return kh::conv3x3(st_, x.p, x.ld, x.C, H, Wd, up, KH_BF16, wt, Kp, Np, bias, res ? res->p : nullptr, y.p, Np, e_, &gws_);
   }
 
   // 1 x 1 conv x.C -> cout (+ residual): a plain GEMM on the activation rows
@@ -172,7 +176,7 @@ class Decoder {
     if ((rc = acquire(x.H, x.W, cout, cout, y))) return rc;
     const kh_weight wt{w, nullptr, KH_BF16, KH_F32, 0};
     if ((rc = gemm(st_, KH_EPI_BIAS16, x.p, KH_BF16, wt, y.p, (int)x.P(), cout, x.C, x.ld, cout, cout, (const float*)b,
-                   e_)))
+                   e_, &gws_)))
       return rc;
     if (res) {
       if (res->ld != y.ld || res->P() != y.P()) return e_.fail("vae: residual shape mismatch");
@@ -228,7 +232,7 @@ class Decoder {
                     (rc = vae_zero(st_, Pm, pl_.Pm, e_))))
       return rc;
     const kh_weight wqkv{wq, nullptr, KH_BF16, KH_F32, 0};
-    if ((rc = gemm(st_, KH_EPI_BIAS16, n.p, KH_BF16, wqkv, qkv, (int)P, 3 * C, C, n.ld, 3 * C, 3 * C, (const float*)bq, e_)))
+    if ((rc = gemm(st_, KH_EPI_BIAS16, n.p, KH_BF16, wqkv, qkv, (int)P, 3 * C, C, n.ld, 3 * C, 3 * C, (const float*)bq, e_, &gws_)))
       return rc;
     release(n);
     if ((rc = vae_transpose(st_, qkv, 3 * C, C, (int)P, C, kt, (int)Pp, e_))) return rc;
@@ -239,11 +243,11 @@ class Decoder {
     for (long long q0 = 0; q0 < P; q0 += pl_.qc) {
       const int rows = (int)std::min<long long>(pl_.qc, P - q0);
       if ((rc = gemm(st_, KH_EPI_F32, qkv + (size_t)q0 * 3 * C, KH_BF16, wk, S, rows, (int)Pp, C, 3 * C, (int)Pp, (int)Pp,
-                     nullptr, e_)))
+                     nullptr, e_, &gws_)))
         return rc;
       if ((rc = vae_softmax(st_, S, (int)Pp, rows, (int)P, scale, Pm, e_))) return rc;
       if ((rc = gemm(st_, KH_EPI_STORE16, Pm, KH_BF16, wv, o.p + (size_t)q0 * C, rows, C, (int)Pp, (int)Pp, 3 * C, C,
-                     nullptr, e_)))
+                     nullptr, e_, &gws_)))
         return rc;
     }
     if ((rc = conv1x1(o, p + "proj", C, &x, y))) return rc;
@@ -256,6 +260,7 @@ class Decoder {
 
 int Decoder::run(const float* z, int H16, int W16, void* rgba) {
   int rc;
+  if (gws_.bytes && (rc = gemm_workspace_init(st_, gws_.p, gws_.bytes, e_))) return rc;
   const void *mean, *stdv, *pw, *pb;
   if ((rc = tensor("latents_mean", KH_F32, 16, -1, mean)) || (rc = tensor("latents_std", KH_F32, 16, -1, stdv)) ||
       (rc = tensor("post_quant_conv.weight", KH_F32, 16, 16, pw)) || (rc = tensor("post_quant_conv.bias", KH_F32, 16, -1, pb)))

@@ -128,7 +128,7 @@ class DitRunner:
     """Weights + buffers of one DiT at a fixed token count (T text rows + H x W image tokens)."""
 
     def __init__(self, shape: DitShape, T: int, H: int, W: int, dev, seed: int = 0,
-                 layers: Optional[List[DitLayerWeights]] = None):
+                 layers: Optional[List[DitLayerWeights]] = None, share: Optional["DitRunner"] = None):
         self.shape, self.dev = shape, dev
         self.T, self.H, self.W = T, H, W
         self.R = R = T + H * W
@@ -143,8 +143,10 @@ class DitRunner:
         self.first_b = 0.01 * torch.randn(D, generator=gen, device=dev)
         self.last_w = 0.02 * torch.randn(D, C, generator=gen, device=dev)
         self.last_b = 0.01 * torch.randn(C, generator=gen, device=dev)
-        self.fin_mul = 1.0 + 0.1 * torch.randn(D, generator=gen, device=dev)
-        self.fin_add = 0.1 * torch.randn(D, generator=gen, device=dev)
+        # final-norm vectors [mul ; add] (StepCond::fin, engine/src/model.h:89-92)
+        self.fin = torch.cat([1.0 + 0.1 * torch.randn(D, generator=gen, device=dev),
+                              0.1 * torch.randn(D, generator=gen, device=dev)]).view(2, D)
+        self.t = torch.zeros(D, device=dev)  # the step's t (Conditioning::get)
         # buffers (engine/src/model.mm:251-267)
         self.x = torch.zeros(R, D, device=dev)
         self.h = torch.empty(R, D, device=dev, dtype=dt)
@@ -155,6 +157,13 @@ class DitRunner:
         self.mods = torch.empty(6 * D, device=dev)
         self.hf = torch.empty(H * W, D, device=dev)
         self.cond = torch.randn(shape.cond_dim or D, generator=gen, device=dev)
+        self.gemm_ws = share.gemm_ws if share is not None else kh.gemm_workspace(dev)  # GEMM stream-K workspace
+        if share is not None:
+            # the same model at another text length (the negative prompt): embed / head weights and the step's
+            # conditioning (tvec, cond, t, final-norm vectors) are the other runner's tensors, so a per-step
+            # update of one conditions both passes (engine/src/pipeline.mm:304-310 passes one conds[i] to both)
+            for name in ("first_w", "first_b", "last_w", "last_b", "fin", "t", "tvec", "cond"):
+                setattr(self, name, getattr(share, name))
         c, s = kh.rope_tables(T, H, W, shape.rope_table_mode)
         self.cos, self.sin = c.to(dev), s.to(dev)
         self.qbig = torch.zeros(R, shape.heads, device=dev)
@@ -162,19 +171,24 @@ class DitRunner:
         self._state = kh.DitStateC(self.x.data_ptr(), self.h.data_ptr(), self.qkv.data_ptr(), self.ao.data_ptr(),
                                    self.mid.data_ptr(), self.tvec.data_ptr(), self.mods.data_ptr(),
                                    self.cond.data_ptr(), self.cond.numel(), self.cos.data_ptr(),
-                                   self.sin.data_ptr(), self.qbig.data_ptr(), self.kbig.data_ptr())
+                                   self.sin.data_ptr(), self.qbig.data_ptr(), self.kbig.data_ptr(),
+                                   self.gemm_ws.data_ptr(), self.gemm_ws.numel())
         self._cfg = shape.config()
 
+    @property
+    def fin_mul(self) -> torch.Tensor:
+        return self.fin[0]
+
+    @property
+    def fin_add(self) -> torch.Tensor:
+        return self.fin[1]
+
     def sibling(self, T: int) -> "DitRunner":
-        """A runner over the same weights, embed / head and conditioning at another text length (the negative
-        prompt of classifier-free guidance, engine/src/pipeline.mm:304-308): its own activation buffers and
-        RoPE tables. The conditioning (cond, tvec) is copied now; refresh it if the step changes it."""
-        r = DitRunner(self.shape, T, self.H, self.W, self.dev, layers=self.layers)
-        for name in ("first_w", "first_b", "last_w", "last_b", "fin_mul", "fin_add"):
-            setattr(r, name, getattr(self, name))
-        r.tvec.copy_(self.tvec)
-        r.cond.copy_(self.cond)
-        return r
+        """A runner over the same weights at another text length (the negative prompt of classifier-free
+        guidance, engine/src/pipeline.mm:304-308): its own activation buffers and RoPE tables; the embed / head
+        weights and the conditioning tensors (tvec, cond, t, fin) are this runner's, so whatever sets the
+        step's conditioning on one sets it on both."""
+        return DitRunner(self.shape, T, self.H, self.W, self.dev, layers=self.layers, share=self)
 
     def run_layers(self, l0: int = 0, l1: Optional[int] = None):
         """DiT::run_layers (engine/src/model.mm:519-525) through kh_dit_forward."""
@@ -193,7 +207,7 @@ class DitRunner:
         self.x[:T].copy_(txt)
         kh.gemm_f32(z, self.first_w, self.x[T:], M, D, C, C, D, D, 1, self.first_b)
         self.run_layers()
-        kh.rms_norm(self.x[T:], self.fin_mul, self.fin_add, self.hf, M, D, D, D, self.shape.eps,
+        kh.rms_norm(self.x[T:], self.fin[0], self.fin[1], self.hf, M, D, D, D, self.shape.eps,
                     self.shape.norm_center)
         kh.gemm_f32(self.hf, self.last_w, vel, M, C, D, D, C, C, 1, self.last_b)
         return vel
@@ -278,14 +292,27 @@ class QwDit(DitRunner):
         self.first_w, self.first_b = f.dev("first.w"), f.dev("first.b")
         self.last_w, self.last_b = f.dev("last.w"), f.dev("last.b")
 
-    def set_cond(self, t: np.ndarray, tvec: np.ndarray):
-        """t [D], tvec [6 D] f32: Conditioning::get's outputs (engine/src/model.mm:545-591) for this step."""
+    def set_cond(self, t, tvec):
+        """t [D], tvec [6 D] f32 (host arrays or device tensors): Conditioning::get's outputs
+        (engine/src/model.mm:545-591) for this step; the final-norm vectors follow on the device (kh_make_fin,
+        DiT::make_cond model.mm:340-346). The per-layer modulation is made inside the layer loop."""
         D = self.shape.dim
-        ln, lm = self.f.array("last.n"), self.f.array("last.mod")
-        t = np.asarray(t, np.float32)
-        self.tvec.copy_(torch.from_numpy(np.ascontiguousarray(tvec, np.float32).reshape(6 * D)))
-        self.fin_mul.copy_(torch.from_numpy((ln * (1.0 + t + lm[0])).astype(np.float32)))
-        self.fin_add.copy_(torch.from_numpy((t + lm[1]).astype(np.float32)))
+        self.t.copy_(torch.as_tensor(np.asarray(t, np.float32) if not torch.is_tensor(t) else t).reshape(D))
+        self.tvec.copy_(torch.as_tensor(np.asarray(tvec, np.float32) if not torch.is_tensor(tvec) else tvec)
+                        .reshape(6 * D))
+        kh.make_fin(self.t, self.f.dev("last.mod"), self.f.dev("last.n"), D, self.fin)
+
+    def set_sigma(self, cond, sigma: float, fast: bool = False) -> bool:
+        """The step's conditioning for noise level sigma from an uploaded cond.qw (`cond`, a QwFile):
+        Conditioning::get (engine/src/model.mm:545-591) on the device (kh_conditioning: table row, or the
+        tmlp / tproj MLP), then the final-norm vectors (kh_make_fin). Returns True on a table hit."""
+        D = self.shape.dim
+        work = self.__dict__.get("_cond_work")
+        if work is None:
+            work = self._cond_work = torch.empty(256 + D, device=self.dev)
+        hit = cond.conditioning(bool(fast), float(sigma), self.t, self.tvec, work)
+        kh.make_fin(self.t, self.f.dev("last.mod"), self.f.dev("last.n"), D, self.fin)
+        return hit
 
 
 def bench_step(dev, rows_img: int = 4096, rows_txt: int = 512, layers: int = 71, steps: int = 3,

@@ -33,7 +33,8 @@ SYMBOLS = ["kh_version", "kh_gemm", "kh_attention", "kh_rms_norm", "kh_qk_norm_r
            "kh_qw_upload", "kh_stream_create", "kh_stream_destroy", "kh_stream_sync", "kh_alloc", "kh_free",
            "kh_upload", "kh_download", "kh_vae_conv3x3", "kh_vae_subpix_weights", "kh_vae_conv_up2", "kh_vae_im2col", "kh_vae_norm_silu", "kh_vae_unpack", "kh_vae_softmax",
            "kh_vae_conv_out", "kh_vae_workspace_bytes", "kh_vae_decode", "kh_gemm_qk_norm_rope",
-           "kh_pack_int8", "kh_sigmas", "kh_euler_step", "kh_cfg_combine", "kh_copy"]
+           "kh_pack_int8", "kh_sigmas", "kh_euler_step", "kh_cfg_combine", "kh_copy", "kh_make_fin", "kh_conditioning",
+           "kh_gemm_ws", "kh_gemm_workspace_bytes", "kh_gemm_workspace_init"]
 
 
 class KhError(RuntimeError):
@@ -64,7 +65,8 @@ class DitStateC(ctypes.Structure):
     _fields_ = [("x", ctypes.c_void_p), ("h", ctypes.c_void_p), ("qkv", ctypes.c_void_p), ("ao", ctypes.c_void_p),
                 ("mid", ctypes.c_void_p), ("tvec", ctypes.c_void_p), ("mods", ctypes.c_void_p),
                 ("cond", ctypes.c_void_p), ("cond_dim", ctypes.c_int), ("cosb", ctypes.c_void_p),
-                ("sinb", ctypes.c_void_p), ("qbig", ctypes.c_void_p), ("kbig", ctypes.c_void_p)]
+                ("sinb", ctypes.c_void_p), ("qbig", ctypes.c_void_p), ("kbig", ctypes.c_void_p),
+                ("gemm_ws", ctypes.c_void_p), ("gemm_ws_bytes", ctypes.c_size_t)]
 
 
 _lib = None
@@ -81,6 +83,12 @@ def load():
         vp, i = ctypes.c_void_p, ctypes.c_int
         lib.kh_gemm.argtypes = [vp, i, vp, i, ctypes.POINTER(_WeightC), vp, i, i, i, i, i, i, vp, ctypes.c_char_p, i]
         lib.kh_gemm.restype = i
+        lib.kh_gemm_ws.argtypes = [vp, i, vp, i, ctypes.POINTER(_WeightC), vp, i, i, i, i, i, i, vp, vp,
+                                   ctypes.c_size_t, ctypes.c_char_p, i]
+        lib.kh_gemm_ws.restype = i
+        lib.kh_gemm_workspace_bytes.argtypes, lib.kh_gemm_workspace_bytes.restype = [], ctypes.c_size_t
+        lib.kh_gemm_workspace_init.argtypes = [vp, vp, ctypes.c_size_t, ctypes.c_char_p, i]
+        lib.kh_gemm_workspace_init.restype = i
         lib.kh_attention.argtypes = [vp, vp, vp, vp, vp, i, i, i, i, i, i, i, i, i, i, i, vp, i, vp, vp,
                                      ctypes.c_char_p, i]
         lib.kh_attention.restype = i
@@ -91,8 +99,11 @@ def load():
         lib.kh_gemv.argtypes = [vp, vp, ctypes.POINTER(_WeightC), vp, i, i, i, i, i, vp, cp, i]
         lib.kh_make_cond.argtypes = [vp, vp, vp, vp, vp, i, vp, cp, i]
         lib.kh_gemm_f32.argtypes = [vp, vp, vp, vp, i, i, i, i, i, i, i, vp, cp, i]
+        lib.kh_make_fin.argtypes, lib.kh_make_fin.restype = [vp, vp, vp, vp, i, vp, cp, i], i
+        lib.kh_conditioning.argtypes = [vp, vp, i, f, vp, vp, vp, ctypes.c_size_t, ctypes.POINTER(i), cp, i]
+        lib.kh_conditioning.restype = i
         lib.kh_gemm_qk_norm_rope.argtypes = ([vp, vp, i, ctypes.POINTER(_WeightC), vp] + [i] * 6 + [vp] * 4 +
-                                             [i] * 4 + [ctypes.c_float, i, i, vp, vp, cp, i])
+                                             [i] * 4 + [ctypes.c_float, i, i, vp, vp, vp, ctypes.c_size_t, cp, i])
         lib.kh_gemm_qk_norm_rope.restype = i
         lib.kh_pack_int8.argtypes, lib.kh_pack_int8.restype = [vp, vp, i, i, vp, cp, i], i
         lib.kh_sigmas.argtypes, lib.kh_sigmas.restype = [i, ctypes.c_float, vp], i
@@ -188,11 +199,23 @@ def _need(t, name: str, rows: int, cols: int, ld: int, esize: int):
         raise KhError(f"gemm: {name} holds {_bytes_after(t)} bytes, the call addresses {need}")
 
 
+def gemm_workspace(dev=None) -> torch.Tensor:
+    """A kh_gemm_ws workspace for the current device (kh_gemm_workspace_bytes, prepared by
+    kh_gemm_workspace_init): uint8 device tensor, owned by the caller; one stream at a time may use it."""
+    lib = load()
+    n = lib.kh_gemm_workspace_bytes()
+    ws = torch.empty(max(int(n), 256), dtype=torch.uint8, device=dev or "cuda")
+    if n:
+        _call(lib.kh_gemm_workspace_init, _stream(), _ptr(ws), ws.numel())
+    return ws
+
+
 def gemm(epi, A: torch.Tensor, W: Weight, C: torch.Tensor, M: int, N: int, K: int, lda: int, ldw: int, ldc: int,
-         vec: Optional[torch.Tensor] = None):
-    """krea::Metal::gemm (engine/src/metal.mm:146-163): acc = A[M,K] x Wt[K,N], then epilogue `epi`.
-    Tensor arguments are checked on the host (dtype of C for the epilogue, storage covering every strided
-    row) so a mis-sized buffer raises instead of reaching the device."""
+         vec: Optional[torch.Tensor] = None, ws: Optional[torch.Tensor] = None):
+    """krea::Metal::gemm (engine/src/metal.mm:146-163): acc = A[M,K] x Wt[K,N], then epilogue `epi`; with `ws`
+    (gemm_workspace()) through kh_gemm_ws, which may run stream-K. Tensor arguments are checked on the host
+    (dtype of C for the epilogue, storage covering every strided row) so a mis-sized buffer raises instead of
+    reaching the device."""
     lib = load()
     if isinstance(epi, str):
         epi = EPI[epi]
@@ -211,13 +234,17 @@ def gemm(epi, A: torch.Tensor, W: Weight, C: torch.Tensor, M: int, N: int, K: in
             _need(vec, "vec", 1, N, N, 4)
     err = ctypes.create_string_buffer(512)
     wc = W.c()
-    rc = lib.kh_gemm(_stream(), epi, _ptr(A), dtype_code(A.dtype), ctypes.byref(wc), _ptr(C), M, N, K, lda, ldw, ldc,
-                     _ptr(vec), err, 512)
+    if ws is None:
+        rc = lib.kh_gemm(_stream(), epi, _ptr(A), dtype_code(A.dtype), ctypes.byref(wc), _ptr(C), M, N, K, lda, ldw,
+                         ldc, _ptr(vec), err, 512)
+    else:
+        rc = lib.kh_gemm_ws(_stream(), epi, _ptr(A), dtype_code(A.dtype), ctypes.byref(wc), _ptr(C), M, N, K, lda,
+                            ldw, ldc, _ptr(vec), _ptr(ws), ws.numel() * ws.element_size(), err, 512)
     _check(rc, err)
     return C
 
 
-def linear(epi, x: torch.Tensor, W: Weight, out: Optional[torch.Tensor] = None, vec=None):
+def linear(epi, x: torch.Tensor, W: Weight, out: Optional[torch.Tensor] = None, vec=None, ws=None):
     """Convenience: contiguous x [M, K] @ W -> out (allocated when None, except residual epilogues)."""
     M, K = x.shape
     N = W.w.shape[1]
@@ -228,7 +255,7 @@ def linear(epi, x: torch.Tensor, W: Weight, out: Optional[torch.Tensor] = None, 
             raise KhError("residual epilogues need the f32 residual tensor as `out`")
         dt = torch.float32 if epi in (EPI["f32"], EPI["bias_f32"]) else x.dtype
         out = torch.empty(M, N // 2 if epi == EPI["swiglu"] else N, dtype=dt, device=x.device)
-    return gemm(epi, x, W, out, M, N, K, x.stride(0), W.w.stride(0), out.stride(0), vec)
+    return gemm(epi, x, W, out, M, N, K, x.stride(0), W.w.stride(0), out.stride(0), vec, ws)
 
 
 def attention(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, O: torch.Tensor, Lq: int, Lk: int, heads: int,
@@ -269,9 +296,9 @@ def qk_norm_rope(qkv: torch.Tensor, wq, wk, cos, sin, rows: int, ld: int, q_off:
 
 def gemm_qk_norm_rope(A: torch.Tensor, W: Weight, C: torch.Tensor, M: int, N: int, K: int, lda: int, ldw: int,
                       ldc: int, wq, wk, cos, sin, q_off: int, n_q: int, k_off: int, n_k: int, eps: float,
-                      rope_mode: int, big_dim: int = -1, qbig=None, kbig=None):
+                      rope_mode: int, big_dim: int = -1, qbig=None, kbig=None, ws=None):
     """The QKV projection of DiT::layer (engine/src/model.mm:373-375) as one launch: kh_gemm STORE16 with
-    kh_qk_norm_rope fused into its epilogue (C plays qkv)."""
+    kh_qk_norm_rope fused into its epilogue (C plays qkv); ws: stream-K workspace (gemm_workspace) or None."""
     if C.dtype != A.dtype:
         raise KhError(f"gemm_qk_norm_rope: C must be {A.dtype}")
     _need(A, "A", M, K, lda, A.element_size())
@@ -280,12 +307,13 @@ def gemm_qk_norm_rope(A: torch.Tensor, W: Weight, C: torch.Tensor, M: int, N: in
     wc = W.c()
     _call(load().kh_gemm_qk_norm_rope, _stream(), _ptr(A), dtype_code(A.dtype), ctypes.byref(wc), _ptr(C), M, N, K,
           lda, ldw, ldc, _ptr(wq), _ptr(wk), _ptr(cos), _ptr(sin), q_off, n_q, k_off, n_k, eps, rope_mode, big_dim,
-          _ptr(qbig), _ptr(kbig))
+          _ptr(qbig), _ptr(kbig), _ptr(ws), 0 if ws is None else ws.numel() * ws.element_size())
     return C
 
 
 def gemv(x: torch.Tensor, W: Weight, y: torch.Tensor, rows: int, N: int, K: int, ldw: int, act: int = 0, bias=None):
-    """gemv_bf16 semantics (engine/kernels/gemm.metal:346-371): y (+)= act(x) W~ + bias."""
+    """gemv_bf16 semantics (engine/kernels/gemm.metal:346-371): y (+)= act(x) W~ + bias; act bit 0 SiLU on load,
+    bit 1 accumulate, bit 2 GELU(tanh) on load (the f32 linears of Conditioning::compute)."""
     wc = W.c()
     _call(load().kh_gemv, _stream(), _ptr(x), ctypes.byref(wc), _ptr(y), rows, N, K, ldw, act, _ptr(bias))
     return y
@@ -295,6 +323,13 @@ def make_cond(tvec, table, n1, n2, D: int, mods):
     """DiT::make_cond (engine/src/model.mm:317-347) for one layer, on the device."""
     _call(load().kh_make_cond, _stream(), _ptr(tvec), _ptr(table), _ptr(n1), _ptr(n2), D, _ptr(mods))
     return mods
+
+
+def make_fin(t, lin, nf, D: int, fin):
+    """The final-norm half of DiT::make_cond (engine/src/model.mm:340-346): fin [2, D] from t [D], last.mod
+    [2, D] and last.n [D], on the device."""
+    _call(load().kh_make_fin, _stream(), _ptr(t), _ptr(lin), _ptr(nf), D, _ptr(fin))
+    return fin
 
 
 def gemm_f32(A, W, C, M: int, N: int, K: int, lda: int, ldw: int, ldc: int, mode: int, bias=None):

@@ -85,49 +85,53 @@ def bf16_bits(x: np.ndarray) -> np.ndarray:
 # ---------------------------------------------------------------------------------------------------------
 # writer
 class QwWriter:
-    """Plans every tensor's offset from (name, dtype, shape) first, then takes the tensors in that order, so
-    a multi-GB file is never held in memory (the contract of tools/convert.py:49-89)."""
+    """A .qw file laid out before any data arrives: every tensor's offset follows from (name, dtype, shape) alone,
+    so the header is final at open and each tensor is written straight to its own offset (positional writes,
+    any order), one at a time: a multi-GB file is never held in memory (the layout of tools/convert.py:49-89).
+    The file appears under its name only once every planned tensor has been written (close)."""
 
     def __init__(self, path: str, specs: Iterable[Tuple[str, str, Tuple[int, ...]]], meta: Optional[dict] = None):
-        self.path, self.tmp = path, path + ".tmp"
-        tensors, self.order, off = {}, [], 0
+        self.path, self.tmp = path, path + ".partial"
+        plan, end = {}, 0
         for name, dtype, shape in specs:
             if dtype not in _SIZE:
                 raise ValueError(f"{name}: unknown dtype {dtype}")
-            if name in tensors:
+            if name in plan:
                 raise ValueError(f"{name}: planned twice")
             nbytes = int(np.prod(shape, dtype=np.int64)) * _SIZE[dtype]
-            tensors[name] = {"dtype": dtype, "shape": [int(s) for s in shape], "offset": off, "nbytes": nbytes}
-            self.order.append(name)
-            off = (off + nbytes + ALIGN - 1) // ALIGN * ALIGN
-        self.header = {"tensors": tensors, "meta": meta or {}}
+            plan[name] = {"dtype": dtype, "shape": [int(s) for s in shape], "offset": end, "nbytes": nbytes}
+            end = -(-(end + nbytes) // ALIGN) * ALIGN
+        self.header = {"tensors": plan, "meta": meta or {}}
         hj = json.dumps(self.header).encode()
-        self.data_start = (16 + len(hj) + ALIGN - 1) // ALIGN * ALIGN
-        self.f = open(self.tmp, "wb")
-        self.f.write(MAGIC + struct.pack("<IQ", VERSION, len(hj)) + hj)
-        self.f.truncate(self.data_start + off)
-        self.next = 0
+        self.data_start = -(-(16 + len(hj)) // ALIGN) * ALIGN
+        self.fd = os.open(self.tmp, os.O_RDWR | os.O_CREAT | os.O_TRUNC, 0o644)
+        os.pwrite(self.fd, MAGIC + struct.pack("<IQ", VERSION, len(hj)) + hj, 0)
+        os.ftruncate(self.fd, self.data_start + end)
+        self.pending = set(plan)
 
     def write(self, name: str, a: np.ndarray):
         """`a`: f32 / f16 / int8 values, or uint16 bf16 bit patterns for a bf16 tensor (f32 input is rounded)."""
-        if self.next >= len(self.order) or self.order[self.next] != name:
-            want = self.order[self.next] if self.next < len(self.order) else "<end>"
-            raise RuntimeError(f"write order: expected {want}, got {name}")
-        info = self.header["tensors"][name]
+        info = self.header["tensors"].get(name)
+        if info is None:
+            raise KeyError(f"{name}: not in the file's plan")
+        if name not in self.pending:
+            raise RuntimeError(f"{name}: already written")
         a = np.asarray(a)
         if info["dtype"] == "bf16" and a.dtype != np.uint16:
             a = bf16_bits(a)
         a = np.ascontiguousarray(a, dtype=_NP[info["dtype"]])
         if list(a.shape) != info["shape"]:
             raise RuntimeError(f"{name}: shape {list(a.shape)} != planned {info['shape']}")
-        self.f.seek(self.data_start + info["offset"])
-        self.f.write(a.tobytes())
-        self.next += 1
+        buf, pos = memoryview(a).cast("B"), self.data_start + info["offset"]
+        while len(buf):
+            n = os.pwrite(self.fd, buf, pos)
+            buf, pos = buf[n:], pos + n
+        self.pending.discard(name)
 
     def close(self):
-        if self.next != len(self.order):
-            raise RuntimeError(f"{self.path}: {len(self.order) - self.next} tensors not written")
-        self.f.close()
+        if self.pending:
+            raise RuntimeError(f"{self.path}: no data for {sorted(self.pending)[:4]} ({len(self.pending)} tensors)")
+        os.close(self.fd)
         os.replace(self.tmp, self.path)
 
 
@@ -156,10 +160,13 @@ def dit_specs(D: int, kv_heads: int, FF: int, layers: int, quant: bool, latent: 
 
 
 def write_random_dit(path: str, D: int, kv_heads: int, FF: int, layers: int, quant: bool = True, seed: int = 0,
-                     big_gain: Optional[Tuple[int, int, float]] = None):
+                     big_gain: Optional[Tuple[int, int, float]] = None, direct_q8: bool = False):
     """A random-init DiT in the converter's layout (the stand-in for dit_q8.qw / dit.qw: no checkpoint is
     available offline). Linear weights ~ N(0, 1/sqrt(K)) in the checkpoint's [out, in] orientation, then
     transposed, fused, interleaved and quantized as convert_dit does (tools/convert.py:190-224).
+    direct_q8 (with quant): the int8 values (uniform in [-127, 127]) and f32 group scales (~1 / (73 sqrt(K)),
+    so the weights' spread is again ~1/sqrt(K)) are drawn directly, which is what a reference-width file
+    (hundreds of millions of weights per layer) needs to be written in seconds; the file layout is the same.
     big_gain = (layer, dim, g): sets qn[dim] = kn[dim] = g in that layer (a high-gain q.k dimension)."""
     rng = np.random.default_rng(seed)
     w = QwWriter(path, dit_specs(D, kv_heads, FF, layers, quant),
@@ -168,6 +175,12 @@ def write_random_dit(path: str, D: int, kv_heads: int, FF: int, layers: int, qua
     kvD = kv_heads * 128
 
     def lin(name, w_out_in):
+        if direct_q8 and quant:
+            N, K = w_out_in
+            w.write(name, rng.integers(-127, 128, (K, N), dtype=np.int8))
+            sc = (1.0 + 0.1 * rng.standard_normal((K // Q_GROUP, N), dtype=np.float32)) / np.float32(73 * np.sqrt(K))
+            w.write(name + ".s", np.abs(sc).astype(np.float32))
+            return
         wt = np.ascontiguousarray(w_out_in.T.astype(np.float32))
         if quant:
             q, s = quantize_q8(wt)
@@ -181,10 +194,16 @@ def write_random_dit(path: str, D: int, kv_heads: int, FF: int, layers: int, qua
 
     for i in range(layers):
         p = f"L{i}."
-        lin(p + "qkvg", np.concatenate([mat(D, D), mat(kvD, D), mat(kvD, D), mat(D, D)]))
-        lin(p + "o", mat(D, D))
-        lin(p + "gu", interleave_gate_up(mat(FF, D), mat(FF, D)))
-        lin(p + "down", mat(D, FF))
+        if direct_q8 and quant:  # (out, in) shapes only
+            lin(p + "qkvg", (2 * D + 2 * kvD, D))
+            lin(p + "o", (D, D))
+            lin(p + "gu", (2 * FF, D))
+            lin(p + "down", (D, FF))
+        else:
+            lin(p + "qkvg", np.concatenate([mat(D, D), mat(kvD, D), mat(kvD, D), mat(D, D)]))
+            lin(p + "o", mat(D, D))
+            lin(p + "gu", interleave_gate_up(mat(FF, D), mat(FF, D)))
+            lin(p + "down", mat(D, FF))
         qn = 1.0 + 0.1 * rng.standard_normal(128, dtype=np.float32)
         kn = 1.0 + 0.1 * rng.standard_normal(128, dtype=np.float32)
         if big_gain is not None and big_gain[0] == i:
@@ -200,6 +219,40 @@ def write_random_dit(path: str, D: int, kv_heads: int, FF: int, layers: int, qua
     w.write("last.b", 0.01 * rng.standard_normal(64, dtype=np.float32))
     w.write("last.n", 1.0 + 0.1 * rng.standard_normal(D, dtype=np.float32))
     w.write("last.mod", 0.1 * rng.standard_normal((2, D), dtype=np.float32))
+    w.close()
+
+
+def cond_specs(D: int, n_base: int, n_fast: int):
+    """(name, dtype, shape) of a cond.qw file (tools/convert.py:287-293)."""
+    return [("tmlp1.w", "f32", (256, D)), ("tmlp1.b", "f32", (D,)), ("tmlp2.w", "f32", (D, D)),
+            ("tmlp2.b", "f32", (D,)), ("tproj.w", "f32", (D, 6 * D)), ("tproj.b", "f32", (6 * D,)),
+            ("base.sigma", "f32", (n_base,)), ("base.t", "f32", (n_base, D)), ("base.tvec", "f32", (n_base, 6 * D)),
+            ("fast.sigma", "f32", (n_fast,)), ("fast.t", "f32", (n_fast, D)), ("fast.tvec", "f32", (n_fast, 6 * D))]
+
+
+def write_random_cond(path: str, D: int, base_sigmas, fast_sigmas, seed: int = 0):
+    """A random-init cond.qw in the converter's layout (the stand-in for the real file, which needs the
+    checkpoint): f32 tmlp1 / tmlp2 / tproj weights ~ N(0, 1/sqrt(in)) stored input-major, small biases, and
+    per-schedule tables whose t / tvec rows are random values (so a table hit is told apart from a computed
+    conditioning)."""
+    rng = np.random.default_rng(seed)
+    base = np.asarray(base_sigmas, np.float32)
+    fast = np.asarray(fast_sigmas, np.float32)
+    w = QwWriter(path, cond_specs(D, len(base), len(fast)), {"model": "krea2-conditioning-random", "seed": seed})
+
+    def mat(i, o):
+        return rng.standard_normal((i, o), dtype=np.float32) / np.float32(np.sqrt(i))
+
+    w.write("tmlp1.w", mat(256, D))
+    w.write("tmlp1.b", 0.1 * rng.standard_normal(D, dtype=np.float32))
+    w.write("tmlp2.w", mat(D, D))
+    w.write("tmlp2.b", 0.1 * rng.standard_normal(D, dtype=np.float32))
+    w.write("tproj.w", mat(D, 6 * D))
+    w.write("tproj.b", 0.1 * rng.standard_normal(6 * D, dtype=np.float32))
+    for tag, sig in (("base", base), ("fast", fast)):
+        w.write(tag + ".sigma", sig)
+        w.write(tag + ".t", rng.standard_normal((len(sig), D), dtype=np.float32))
+        w.write(tag + ".tvec", 0.2 * rng.standard_normal((len(sig), 6 * D), dtype=np.float32))
     w.close()
 
 
@@ -337,6 +390,17 @@ class QwFile:
         rc = self.lib.kh_qw_upload(self.h, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream), err, 512)
         kh._check(rc, err)
         return self
+
+    def conditioning(self, fast: bool, sigma: float, t, tvec, work) -> bool:
+        """kh_conditioning on this (uploaded) cond.qw: t [D] and tvec [6 D] (f32 device tensors) for noise level
+        sigma, Conditioning::get / compute (engine/src/model.mm:545-591); work: f32 device scratch of >= 256 + D
+        floats. Returns True when the sigma was found in the schedule's table."""
+        hit = ctypes.c_int(0)
+        err = ctypes.create_string_buffer(512)
+        rc = kh.load().kh_conditioning(kh._stream(), self.h, int(fast), float(sigma), kh._ptr(t), kh._ptr(tvec),
+                                       kh._ptr(work), work.numel() * work.element_size(), ctypes.byref(hit), err, 512)
+        kh._check(rc, err)
+        return bool(hit.value)
 
     def dev(self, name: str) -> DevPtr:
         ti = self.info(name)

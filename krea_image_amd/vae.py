@@ -110,9 +110,9 @@ def _bind(lib):
     lib.kh_vae_decode.argtypes = [vp, vp, vp, i, i, vp, sz, vp, cp, i]
     lib.kh_vae_decode.restype = i
     lib.kh_vae_im2col.argtypes = [vp, vp, i, i, i, i, i, i, i, vp, i, cp, i]
-    lib.kh_vae_conv3x3.argtypes = [vp, vp, i, i, i, i, i, i, vp, i, i, vp, vp, vp, i, cp, i]
+    lib.kh_vae_conv3x3.argtypes = [vp, vp, i, i, i, i, i, i, vp, i, i, vp, vp, vp, i, vp, ctypes.c_size_t, cp, i]
     lib.kh_vae_subpix_weights.argtypes = [vp, vp, i, i, i, vp, i, i, vp, vp, cp, i]
-    lib.kh_vae_conv_up2.argtypes = [vp, vp, i, i, i, i, i, vp, i, i, vp, vp, i, cp, i]
+    lib.kh_vae_conv_up2.argtypes = [vp, vp, i, i, i, i, i, vp, i, i, vp, vp, i, vp, ctypes.c_size_t, cp, i]
     lib.kh_vae_norm_silu.argtypes = [vp, vp, i, vp, vp, i, i, i, i, cp, i]
     lib.kh_vae_unpack.argtypes = [vp] * 7 + [i, i, cp, i]
     lib.kh_vae_softmax.argtypes = [vp, vp, i, i, i, ctypes.c_float, vp, cp, i]
@@ -132,7 +132,15 @@ def _dp(t):
     return ctypes.c_void_p(t.data_ptr() if hasattr(t, "data_ptr") else int(t))
 
 
-def conv3x3(x, ldx, C, H, W, up, w, K, N, bias, y, ldy, res=None):
+def _ws(ws):
+    return None if ws is None else _dp(ws)
+
+
+def _ws_bytes(ws) -> int:
+    return 0 if ws is None else ws.numel() * ws.element_size()
+
+
+def conv3x3(x, ldx, C, H, W, up, w, K, N, bias, y, ldy, res=None, ws=None):
     """VAEDecoder::conv mode 3 (engine/src/vae.mm:112-125): implicit-GEMM 3x3 conv, y = conv(x) + bias
     (+ res, added after the 16-bit rounding of the biased output). w: 16-bit Wt [K, N] (K >= 9 C, a multiple
     of 64); H x W output pixels (up: x is H/2 x W/2); res like y."""
@@ -149,7 +157,7 @@ def conv3x3(x, ldx, C, H, W, up, w, K, N, bias, y, ldy, res=None):
         raise kh.KhError("conv3x3: x, w and y share one 16-bit type; bias is f32")
     wc = kh.Weight(w).c()
     _call(_bind(kh.load()).kh_vae_conv3x3, kh._stream(), _dp(x), ldx, C, H, W, up, kh.dtype_code(x.dtype),
-          ctypes.byref(wc), K, N, _dp(bias), None if res is None else _dp(res), _dp(y), ldy)
+          ctypes.byref(wc), K, N, _dp(bias), None if res is None else _dp(res), _dp(y), ldy, _ws(ws), _ws_bytes(ws))
 
 
 def subpix_weights(w, Cin, Cout, w2, K, Np, bias=None, bias4=None):
@@ -162,7 +170,7 @@ def subpix_weights(w, Cin, Cout, w2, K, Np, bias=None, bias4=None):
           Np, None if bias is None else _dp(bias), None if bias4 is None else _dp(bias4))
 
 
-def conv_up2(x, ldx, C, H, W, w2, K, Np, bias4, y, ldy):
+def conv_up2(x, ldx, C, H, W, w2, K, Np, bias4, y, ldy, ws=None):
     """VAEDecoder::conv mode 2 (engine/src/vae.mm:137-150): y [(2H)(2W), ldy] = conv3x3(nearest2x(x)) + bias
     as four sub-pixel 2 x 2 convs; x [H W, ldx] low-res, w2 / bias4 from subpix_weights."""
     kh._need(x, "x", H * W, C, ldx, x.element_size())
@@ -173,7 +181,7 @@ def conv_up2(x, ldx, C, H, W, w2, K, Np, bias4, y, ldy):
         raise kh.KhError("conv_up2: x, w2 and y share one 16-bit type")
     wc = kh.Weight(w2).c()
     _call(_bind(kh.load()).kh_vae_conv_up2, kh._stream(), _dp(x), ldx, C, H, W, kh.dtype_code(x.dtype),
-          ctypes.byref(wc), K, Np, _dp(bias4), _dp(y), ldy)
+          ctypes.byref(wc), K, Np, _dp(bias4), _dp(y), ldy, _ws(ws), _ws_bytes(ws))
 
 
 def im2col(x, ldx, C, H, W, up, m0, rows, col, Kpad):

@@ -12,7 +12,10 @@
  *   or_gemm                 fp64 brute force (numpy) on small shapes for every epilogue and weight format;
  *                           identity-weight and permutation-weight invariants; K-split additivity;
  *                           torch gelu(approximate="tanh") and torch silu for the epilogue functions.
- *   or_gemv                 numpy fp64 matvec.
+ *   or_gemv                 numpy fp64 matvec; torch silu / gelu(approximate="tanh") for the on-load activations.
+ *   or_temb                 closed forms: sigma = 0 gives cos = 1, sin = 0; numpy float64 of the same formula
+ *                           at bf16(sigma) (<= 1e-5 absolute); bf16 rounding of sigma checked against torch.
+ *   or_make_fin             numpy restatement of model.mm:340-346 on random vectors.
  *   or_make_cond            numpy restatement of model.mm:329-338 on random vectors.
  *   or_rms_norm             numpy fp64; torch layer_norm for center = 1.
  *   or_qk_norm_rope         complex-multiplication form of RoPE (numpy); rotate-half vs pairs equivalence
@@ -320,7 +323,10 @@ int or_gemv(const float* x, const void* w, int w_dtype, const void* s, int s_dty
   for (int r = 0; r < rows; r++) {
     float* xa = (float*)malloc(sizeof(float) * (size_t)K);
     if (!xa) return -1;
-    for (int k = 0; k < K; k++) xa[k] = (act & 1) ? silu_f(x[(size_t)r * K + k]) : x[(size_t)r * K + k];
+    for (int k = 0; k < K; k++) {
+      const float v = x[(size_t)r * K + k];
+      xa[k] = (act & 1) ? silu_f(v) : (act & 4) ? gelu_tanh_f(v) : v;
+    }
 #pragma omp parallel for schedule(static)
     for (int n = 0; n < N; n++) {
       double acc = 0.0;
@@ -337,6 +343,26 @@ int or_gemv(const float* x, const void* w, int w_dtype, const void* s, int s_dty
     free(xa);
   }
   return 0;
+}
+
+/* Timestep embedding of Conditioning::compute (engine/src/model.mm:576-581): e[i] = cos(ts 1000 f_i),
+ * e[128 + i] = sin(ts 1000 f_i), f_i = exp(-log(10000) i / 128), ts = bf16(sigma); float arithmetic as written
+ * there. */
+void or_temb(float sigma, float* e) {
+  const float ts = or_bf16_to_f32(or_f32_to_bf16(sigma));
+  for (int i = 0; i < 128; i++) {
+    const float f = expf(-logf(10000.0f) * (float)i / 128.0f);
+    e[i] = cosf(ts * 1000.0f * f);
+    e[128 + i] = sinf(ts * 1000.0f * f);
+  }
+}
+
+/* engine/src/model.mm:340-346 (the final-norm vectors of DiT::make_cond) */
+void or_make_fin(const float* t, const float* lin, const float* nf, int D, float* fin) {
+  for (int k = 0; k < D; k++) {
+    fin[k] = nf[k] * (1.0f + t[k] + lin[k]);
+    fin[D + k] = t[k] + lin[D + k];
+  }
 }
 
 /* engine/src/model.mm:329-338 */

@@ -51,6 +51,10 @@ int or_gemm(int epi, const void* A, int a_dtype, const void* w, int w_dtype, con
  * y[r,n] = (y if act&2) + sum_k act1(x[r,k]) W~[k,n] (+ bias[n]); act&1 = SiLU on load. x, y f32. */
 int or_gemv(const float* x, const void* w, int w_dtype, const void* s, int s_dtype, int group, float* y, int rows,
             int N, int K, int ldw, int act, const float* bias);
+/* engine/src/model.mm:576-581: timestep embedding e[256] of bf16(sigma). */
+void or_temb(float sigma, float* e);
+/* engine/src/model.mm:340-346: fin[2 D] from t [D], lin [2 D], nf [D]. */
+void or_make_fin(const float* t, const float* lin, const float* nf, int D, float* fin);
 
 /* engine/src/model.mm:317-347 (DiT::make_cond), one layer: v_j = tvec[j*D + k] (+ table[j*D + k]);
  * mods = [n1 (1 + v0), v1, v2, n2 (1 + v3), v4, v5]. */

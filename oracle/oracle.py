@@ -49,6 +49,8 @@ def lib():
         _lib.or_vae_unpack.argtypes = [vp] * 6 + [i, i]
         _lib.or_vae_softmax.argtypes = [vp, i, i, i, ctypes.c_float, vp]
         _lib.or_vae_conv_out.argtypes = [vp, i, vp, vp, vp, i, i]
+        _lib.or_temb.argtypes = [ctypes.c_float, vp]
+        _lib.or_make_fin.argtypes = [vp, vp, vp, i, vp]
     return _lib
 
 
@@ -170,6 +172,33 @@ def gemv(x, w, w_dtype, s=None, s_dtype=F32, group=0, y=None, act=0, bias=None):
     if rc != 0:
         raise ValueError("oracle gemv: bad shape")
     return y
+
+
+def temb(sigma: float) -> np.ndarray:
+    """Timestep embedding of Conditioning::compute (engine/src/model.mm:576-581): f32 [256] of bf16(sigma)."""
+    e = np.empty(256, np.float32)
+    lib().or_temb(float(sigma), _p(e))
+    return e
+
+
+def make_fin(t, lin, nf):
+    """Final-norm vectors of DiT::make_cond (engine/src/model.mm:340-346): f32 [2, D]."""
+    D = nf.shape[0]
+    fin = np.empty((2, D), np.float32)
+    lib().or_make_fin(_p(np.ascontiguousarray(t, np.float32)), _p(np.ascontiguousarray(lin, np.float32)),
+                      _p(np.ascontiguousarray(nf, np.float32)), D, _p(fin))
+    return fin
+
+
+def conditioning(sigma: float, w1, b1, w2, b2, wp, bp):
+    """Conditioning::compute (engine/src/model.mm:571-591): (t [D], tvec [6 D]) f32 from the f32 tmlp1 [256, D],
+    tmlp2 [D, D], tproj [D, 6 D] weights (input-major) and biases, as a composition of the oracle's gemv
+    (GELU(tanh) on load, act bit 2) on temb(sigma)."""
+    e = temb(sigma)[None]
+    h = gemv(e, np.ascontiguousarray(w1, np.float32), F32, bias=b1)
+    t = gemv(h, np.ascontiguousarray(w2, np.float32), F32, bias=b2, act=4)
+    tvec = gemv(t, np.ascontiguousarray(wp, np.float32), F32, bias=bp, act=4)
+    return t[0], tvec[0]
 
 
 def make_cond(tvec, table, n1, n2):

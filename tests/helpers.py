@@ -73,3 +73,14 @@ def host_int8(W):
     """The input-major int8 matrix of a kh.Weight, packed or not, as numpy."""
     q = W.w.cpu().numpy()
     return unpack_int8(q) if getattr(W, "packed", False) else q
+
+
+_WS = {}
+
+
+def gemm_ws(dev):
+    """One kh_gemm_ws stream-K workspace per device for the tests (kh.gemm_workspace)."""
+    from krea_image_amd import kh
+    if dev not in _WS:
+        _WS[dev] = kh.gemm_workspace(dev)
+    return _WS[dev]

@@ -104,3 +104,42 @@ def test_gemm_front_end_rejects_wrong_output_dtype_and_short_buffers():
         kh.gemm("store16", A, W, C, 256, 64, 128, 128, 64, 128)
     with pytest.raises(kh.KhError, match="vec holds"):
         kh.gemm("bias_f32", A, W, torch.zeros(256, 64), 256, 64, 128, 128, 64, 64, torch.zeros(32))
+
+
+def test_gemm_rejects_activation_offsets_past_2pow31(lib):
+    """262145 rows of K = lda = 8192: (M - 1) * lda + K = 2^31 + 8192 overflows the 32-bit activation offsets;
+    rejected before any launch (the pointers are never dereferenced)."""
+    rc, err = _gemm_call(lib, M=262145, K=8192, lda=8192, N=256, ldw=256, ldc=256)
+    assert rc == -1 and "2^31" in err, err
+    rc, err = _gemm_call(lib, M=262144, K=8192, lda=8192, N=256, ldw=256, ldc=256, A=0)
+    assert rc == -1 and "null" in err  # one row fewer passes the offset check (and stops at the null A)
+
+
+def test_gemm_ws_rejects_unaligned_workspace(lib):
+    from krea_image_amd import kh
+    err = ctypes.create_string_buffer(256)
+    w = kh._WeightC(16, 16, kh.I8, kh.F16, 0)
+    rc = lib.kh_gemm_ws(None, 0, ctypes.c_void_p(16), kh.F16, ctypes.byref(w), ctypes.c_void_p(16), 64, 64, 64, 64,
+                        64, 64, None, ctypes.c_void_p(16 + 64), 1 << 20, err, 256)
+    assert rc == -1 and "256-byte aligned" in err.value.decode()
+
+
+def test_gemv_rejects_without_launch(lib):
+    from krea_image_amd import kh
+    err = ctypes.create_string_buffer(256)
+    w = kh._WeightC(16, 0, kh.F32, kh.F32, 0)
+    p = ctypes.c_void_p(16)
+    assert lib.kh_gemv(None, p, ctypes.byref(w), p, 1, 64, 64, 64, 5, None, err, 256) == -1
+    assert "exclusive" in err.value.decode()
+    assert lib.kh_gemv(None, p, ctypes.byref(w), p, 5, 64, 64, 64, 0, None, err, 256) == -1
+    assert "rows" in err.value.decode()
+    assert lib.kh_gemv(None, p, ctypes.byref(w), p, 1, 66, 64, 66, 0, None, err, 256) == -1
+    assert "multiple of 4" in err.value.decode()
+
+
+def test_conditioning_and_make_fin_reject_null(lib):
+    err = ctypes.create_string_buffer(256)
+    p = ctypes.c_void_p(16)
+    rc = lib.kh_conditioning(None, None, 0, ctypes.c_float(0.5), p, p, p, 4096, None, err, 256)
+    assert rc == -1 and "null" in err.value.decode()
+    assert lib.kh_make_fin(None, None, p, p, 64, p, err, 256) == -1

@@ -10,7 +10,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
-from tests.helpers import from_dev16, make_weight, randn16, rel_l2, to_dev16, weight_to_dev
+from tests.helpers import from_dev16, gemm_ws, make_weight, randn16, rel_l2, to_dev16, weight_to_dev
 
 pytestmark = pytest.mark.gpu
 TOL = 5e-3
@@ -18,9 +18,11 @@ EPIS = ["store16", "f32", "resid_gate", "resid", "swiglu", "gelu", "bias16", "bi
 F32_OUT = {"f32", "resid_gate", "resid", "bias_f32"}
 
 
-def run_case(dev, a_dtype, kind, epi, M, N, K, seed=0, rows=None):
+def run_case(dev, a_dtype, kind, epi, M, N, K, seed=0, rows=None, ws=True):
+    """One GEMM against the oracle; ws=True goes through kh_gemm_ws with a stream-K workspace (stream-K where
+    the plan picks it), ws=False through kh_gemm (data-parallel always)."""
     from krea_image_amd import kh
-    print(f"[gemm case] a_dtype={a_dtype} w={kind} epi={epi} M={M} N={N} K={K} seed={seed}", flush=True)
+    print(f"[gemm case] a_dtype={a_dtype} w={kind} epi={epi} M={M} N={N} K={K} seed={seed} ws={ws}", flush=True)
     rng = np.random.default_rng(seed)
     A = randn16(rng, (M, K), a_dtype)
     wd = make_weight(rng, K, N, kind, a_dtype)
@@ -35,7 +37,7 @@ def run_case(dev, a_dtype, kind, epi, M, N, K, seed=0, rows=None):
         Cd = torch.from_numpy(C0.copy()).to(dev)
     else:
         Cd = torch.zeros(M, ncol, dtype=Ad.dtype, device=dev)
-    kh.gemm(epi, Ad, W, Cd, M, N, K, K, N, ncol, vd)
+    kh.gemm(epi, Ad, W, Cd, M, N, K, K, N, ncol, vd, gemm_ws(dev) if ws else None)
     torch.cuda.synchronize()
     got = Cd.cpu().numpy() if epi in F32_OUT else O.to_f32(from_dev16(Cd), a_dtype)
 
@@ -178,8 +180,8 @@ def test_gemm_rows_past_m_untouched(dev, epi, packed):
 
 def test_gemm_activation_offsets_near_2pow31(dev):
     """Largest A the 32-bit activation offsets allow: (M - 1) * lda + K = 2146304000 < 2^31 (A is 4.3 GB of fp16).
-    Rows spread over the whole range, the last rows included, against the oracle; one row past the limit is
-    rejected."""
+    Rows spread over the whole range, the last rows included, against the oracle (the rejection one row past
+    the limit is a CPU test: tests/test_abi.py)."""
     from krea_image_amd import kh
     M, K, N = 262000, 8192, 256
     g = torch.Generator(device=dev)
@@ -199,10 +201,3 @@ def test_gemm_activation_offsets_near_2pow31(dev):
     assert rel_l2(got, ref) <= TOL
     del A, C
     torch.cuda.empty_cache()
-    # 262145 rows: (M - 1) * lda + K = 2^31 + 8192, rejected before any launch (no buffers are touched)
-    import ctypes
-    err = ctypes.create_string_buffer(256)
-    wc = W.c()
-    rc = kh.load().kh_gemm(kh._stream(), 0, ctypes.c_void_p(16), 1, ctypes.byref(wc), ctypes.c_void_p(16), 262145, N,
-                           K, K, N, N, None, err, 256)
-    assert rc != 0 and "2^31" in err.value.decode()

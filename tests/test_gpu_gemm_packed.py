@@ -7,7 +7,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
-from tests.helpers import make_weight, randn16, rel_l2, to_dev16, weight_to_dev
+from tests.helpers import gemm_ws, make_weight, randn16, rel_l2, to_dev16, weight_to_dev
 from tests.test_gpu_gemm import F32_OUT
 
 pytestmark = pytest.mark.gpu
@@ -43,7 +43,7 @@ def _both(dev, a_dtype, kind, epi, M, N, K, seed):
     outs = []
     for w in (W, W.pack()):
         C = C0.clone() if C0 is not None else torch.zeros(M, ncol, dtype=A.dtype, device=dev)
-        kh.gemm(epi, A, w, C, M, N, K, K, N, ncol, vec)
+        kh.gemm(epi, A, w, C, M, N, K, K, N, ncol, vec, gemm_ws(dev))
         torch.cuda.synchronize()
         outs.append(C.cpu())
     return outs

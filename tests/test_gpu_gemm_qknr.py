@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
-from tests.helpers import from_dev16, make_weight, randn16, rel_l2, to_dev16, weight_to_dev
+from tests.helpers import from_dev16, gemm_ws, make_weight, randn16, rel_l2, to_dev16, weight_to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -38,9 +38,9 @@ def _case(dev, dtype, kind, rope_mode, big_dim, nq, nk, gate, M, K, seed):
     tdt = torch.float16 if dtype == O.F16 else torch.bfloat16
     C1 = torch.empty(M, N, dtype=tdt, device=dev)
     kh.gemm_qk_norm_rope(Ad, W, C1, M, N, K, K, N, N, wqd, wkd, cd, sd, 0, nq, nq * 128, nk, 1e-5, rope_mode, big_dim,
-                         qb1 if big else None, kb1 if big else None)
+                         qb1 if big else None, kb1 if big else None, ws=gemm_ws(dev))
     C2 = torch.empty(M, N, dtype=tdt, device=dev)
-    kh.gemm("store16", Ad, W, C2, M, N, K, K, N, N)
+    kh.gemm("store16", Ad, W, C2, M, N, K, K, N, N, ws=gemm_ws(dev))
     kh.qk_norm_rope(C2, wqd, wkd, cd, sd, M, N, 0, nq, nq * 128, nk, 1e-5, rope_mode, big_dim,
                     qb2 if big else None, kb2 if big else None)
     torch.cuda.synchronize()

@@ -10,7 +10,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
-from tests.helpers import make_weight, randn16, to_dev16, weight_to_dev
+from tests.helpers import gemm_ws, make_weight, randn16, to_dev16, weight_to_dev
 from tests.test_gpu_gemm import EPIS, F32_OUT, run_case
 
 pytestmark = pytest.mark.gpu
@@ -43,7 +43,7 @@ def test_tn192_matches_256_wide_bitwise(dev, epi):
 
     def run():
         C = C0.clone() if epi in F32_OUT else torch.zeros(M, N, dtype=torch.float16, device=dev)
-        kh.gemm(epi, A, W, C, M, N, K, K, N, N, vec)
+        kh.gemm(epi, A, W, C, M, N, K, K, N, N, vec, gemm_ws(dev))
         torch.cuda.synchronize()
         return C.cpu()
 
@@ -81,7 +81,7 @@ def test_narrow_matches_256_wide_bitwise(dev, kind, N):
 
     def run():
         C = torch.zeros(Mr, N, dtype=torch.bfloat16, device=dev)
-        kh.gemm("bias16", A, W, C, Mr, N, K, K, N, N, vec)
+        kh.gemm("bias16", A, W, C, Mr, N, K, K, N, N, vec, gemm_ws(dev))
         torch.cuda.synchronize()
         return C.cpu()
 

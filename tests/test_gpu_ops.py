@@ -1,6 +1,7 @@
 """Parity of the ops around the GEMMs (kh_rms_norm, kh_qk_norm_rope, kh_gemv, kh_make_cond, kh_gemm_f32)
 against the CPU oracle, through the C ABI. Tolerances: one 16-bit rounding of the outputs (<= 0.5 % rel L2);
-f32 outputs 1e-5; the GEMV sums in a different order (atomics) -> 1e-5."""
+f32 outputs 1e-5 (the GEMV sums in another order than the oracle's float64); the GEMV and the fp32 GEMM repeat
+bit for bit."""
 import numpy as np
 import pytest
 import torch
@@ -73,12 +74,16 @@ def test_qk_norm_rope_big_dim(dev):
     assert rel_l2(qb.cpu().numpy(), rqb) < 1e-5 and rel_l2(kb.cpu().numpy(), rkb) < 1e-5
 
 
-@pytest.mark.parametrize("kind", ["ch", "g128", "16"])
-@pytest.mark.parametrize("act", [0, 1, 3])
-def test_gemv(dev, kind, act):
+@pytest.mark.parametrize("kind", ["ch", "g128", "16", "f32"])
+@pytest.mark.parametrize("act", [0, 1, 3, 4, 6])
+@pytest.mark.parametrize("rows", [1, 3])
+def test_gemv(dev, kind, act, rows):
+    """kh_gemv against the oracle (<= 1e-5 relative L2) for every weight format, SiLU / GELU on load and the
+    accumulate bit; the output repeats bit for bit (fixed-order reduction, no atomics)."""
     from krea_image_amd import kh
-    rng = np.random.default_rng(11 + act)
-    rows, K, N = 2, 3072, 18432 if kind == "ch" else 1024
+    rng = np.random.default_rng(11 + act + 7 * rows)
+    K, N = (3072, 18432) if kind == "ch" else (1024, 1040) if kind == "f32" else (3072, 1024)
+    print(f"[gemv] {kind} act={act} rows={rows} K={K} N={N}", flush=True)
     x = rng.standard_normal((rows, K)).astype(np.float32)
     bias = rng.standard_normal(N).astype(np.float32)
     if kind == "ch":
@@ -90,16 +95,33 @@ def test_gemv(dev, kind, act):
         w, s = O.quant_q8((rng.standard_normal((K, N)) * 0.02).astype(np.float32), 128)
         W = kh.Weight(torch.from_numpy(w).to(dev), torch.from_numpy(s).to(dev), 128)
         wargs = (w, O.I8, s, O.F32, 128)
-    else:
+    elif kind == "16":
         w = O.from_f32((rng.standard_normal((K, N)) * 0.02).astype(np.float32), O.BF16)
         W = kh.Weight(to_dev16(w, O.BF16, dev))
         wargs = (w, O.BF16, None, O.F32, 0)
+    else:
+        w = (rng.standard_normal((K, N)) / np.sqrt(K)).astype(np.float32)
+        W = kh.Weight(torch.from_numpy(w).to(dev))
+        wargs = (w, O.F32, None, O.F32, 0)
     y0 = rng.standard_normal((rows, N)).astype(np.float32)
-    y = torch.from_numpy(y0.copy()).to(dev)
-    kh.gemv(torch.from_numpy(x).to(dev), W, y, rows, N, K, N, act, torch.from_numpy(bias).to(dev))
-    torch.cuda.synchronize()
+    xd, bd = torch.from_numpy(x).to(dev), torch.from_numpy(bias).to(dev)
+    outs = []
+    for _ in range(2):
+        y = torch.from_numpy(y0.copy()).to(dev)
+        kh.gemv(xd, W, y, rows, N, K, N, act, bd)
+        torch.cuda.synchronize()
+        outs.append(y.cpu())
+    assert torch.equal(outs[0], outs[1])
     ref = O.gemv(x, *wargs, y=y0.copy(), act=act, bias=bias)
-    assert rel_l2(y.cpu().numpy(), ref) < 1e-5
+    assert rel_l2(outs[0].numpy(), ref) < 1e-5
+
+
+def test_gemv_rejects_bad_act(dev):
+    from krea_image_amd import kh
+    W = kh.Weight(torch.zeros(64, 64, device=dev))
+    x, y = torch.zeros(1, 64, device=dev), torch.zeros(1, 64, device=dev)
+    with pytest.raises(kh.KhError, match="exclusive"):
+        kh.gemv(x, W, y, 1, 64, 64, 64, 5)
 
 
 def test_make_cond(dev):
@@ -133,3 +155,23 @@ def test_gemm_f32(dev, mode):
         v = torch.nn.functional.gelu(torch.from_numpy(v), approximate="tanh").numpy()
     ref = C0 + v if mode & 4 else v
     assert rel_l2(C.cpu().numpy(), ref) < 1e-5
+
+
+def test_gemm_f32_head_shape_repeatable(dev):
+    """The D -> 64 head at 4096 rows (16-row tiles, each output summed over all of K by one thread): against
+    float64 and bit for bit across two runs."""
+    from krea_image_amd import kh
+    rng = np.random.default_rng(33)
+    M, K, N = 4096, 3072, 64
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    W = (rng.standard_normal((K, N)) * 0.02).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    Ad, Wd, bd = (torch.from_numpy(v).to(dev) for v in (A, W, b))
+    outs = []
+    for _ in range(2):
+        C = torch.empty(M, N, device=dev)
+        kh.gemm_f32(Ad, Wd, C, M, N, K, K, N, N, 1, bd)
+        torch.cuda.synchronize()
+        outs.append(C.cpu())
+    assert torch.equal(outs[0], outs[1])
+    assert rel_l2(outs[0].numpy(), A.astype(np.float64) @ W + b) < 1e-5

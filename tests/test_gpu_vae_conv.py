@@ -9,6 +9,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
+from tests.helpers import gemm_ws
 
 pytestmark = pytest.mark.gpu
 
@@ -44,18 +45,18 @@ def test_conv3x3_implicit(dev, H, W, C, N, up):
     xd, wd, bd = _dev16(x, dev), _dev16(w, dev), torch.from_numpy(bias).to(dev)
     P = H * W
     y = torch.empty(P, N, dtype=torch.bfloat16, device=dev)
-    vae.conv3x3(xd, ldx, C, H, W, up, wd, K, N, bd, y, N)
+    vae.conv3x3(xd, ldx, C, H, W, up, wd, K, N, bd, y, N, ws=gemm_ws(dev))
     col = torch.empty(P, K, dtype=torch.bfloat16, device=dev)
     vae.im2col(xd, ldx, C, H, W, up, 0, P, col, K)
     y2 = torch.empty(P, N, dtype=torch.bfloat16, device=dev)
-    kh.gemm("bias16", col, kh.Weight(wd), y2, P, N, K, K, N, N, bd)
+    kh.gemm("bias16", col, kh.Weight(wd), y2, P, N, K, K, N, N, bd, gemm_ws(dev))
     torch.cuda.synchronize()
     got = y.view(torch.int16).cpu().numpy().view(np.uint16)
     np.testing.assert_array_equal(got, y2.view(torch.int16).cpu().numpy().view(np.uint16))
     # fused residual: round16(round16(conv + bias) + res), bit for bit
     R = _bf(rng.standard_normal((P, N)))
     y3 = torch.empty(P, N, dtype=torch.bfloat16, device=dev)
-    vae.conv3x3(xd, ldx, C, H, W, up, wd, K, N, bd, y3, N, res=_dev16(R, dev))
+    vae.conv3x3(xd, ldx, C, H, W, up, wd, K, N, bd, y3, N, res=_dev16(R, dev), ws=gemm_ws(dev))
     torch.cuda.synchronize()
     want = O.from_f32(O.to_f32(got, O.BF16) + O.to_f32(R, O.BF16), O.BF16)
     np.testing.assert_array_equal(y3.view(torch.int16).cpu().numpy().view(np.uint16), want)
@@ -97,7 +98,7 @@ def test_conv_up2_subpixel(dev, H, W, C, Cout):
     b4 = torch.empty(4 * Np, device=dev)
     vae.subpix_weights(wd, C, Cout, w2, K, Np, bd, b4)
     y = torch.empty(4 * H * W, Np, dtype=torch.bfloat16, device=dev)
-    vae.conv_up2(xd, C, C, H, W, w2, K, Np, b4, y, Np)
+    vae.conv_up2(xd, C, C, H, W, w2, K, Np, b4, y, Np, ws=gemm_ws(dev))
     torch.cuda.synchronize()
     ref_w2 = O.vae_subpix_weights(w, C, Cout)
     got_w2 = w2.view(torch.int16).cpu().numpy().view(np.uint16)

@@ -213,6 +213,73 @@ def test_gemv_silu_int8_channel():
     assert rel_l2(y2, 2 * ref) < 1e-6
 
 
+def test_gemv_gelu_on_load_f32_weights():
+    """act bit 2: GELU(tanh) of x on load (Conditioning::compute's gelu between its linears), torch's
+    gelu(approximate="tanh") in float64 as the reference; f32 weights."""
+    rng = np.random.default_rng(41)
+    K, N = 192, 40
+    x = (2 * rng.standard_normal((3, K))).astype(np.float32)
+    w = rng.standard_normal((K, N)).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    y = O.gemv(x, w, O.F32, act=4, bias=b)
+    g = torch.nn.functional.gelu(torch.from_numpy(x).double(), approximate="tanh").numpy()
+    assert rel_l2(y, g @ w.astype(np.float64) + b) < 1e-6
+
+
+def _bf16(v: float) -> float:
+    return float(torch.tensor(v, dtype=torch.float32).to(torch.bfloat16).float())
+
+
+def test_temb_closed_forms():
+    """engine/src/model.mm:576-581. sigma = 0: every cos term is 1 and every sin term 0. Any sigma: the values
+    are cos / sin of bf16(sigma) * 1000 * 10000^(-i/128) (argument formed in float32 as the reference writes
+    it; numpy float64 trig), and within 2e-4 of the all-float64 formula (the float32 argument's rounding)."""
+    e = O.temb(0.0)
+    assert np.array_equal(e[:128], np.ones(128, np.float32)) and np.array_equal(e[128:], np.zeros(128, np.float32))
+    i = np.arange(128, dtype=np.float32)
+    for sig in (1.0, 0.8123, 0.3333, 0.0421):
+        ts = np.float32(_bf16(sig))
+        # float32 exponent, then a correctly rounded float32 exp (float64 exp, one rounding)
+        ex = (-np.float32(np.log(10000.0)) * i) / np.float32(128.0)
+        fr = np.exp(ex.astype(np.float64)).astype(np.float32)
+        arg = (ts * np.float32(1000.0)) * fr
+        got = O.temb(sig)
+        assert np.abs(got[:128] - np.cos(arg.astype(np.float64))).max() <= 2e-6
+        assert np.abs(got[128:] - np.sin(arg.astype(np.float64))).max() <= 2e-6
+        a64 = _bf16(sig) * 1000.0 * np.exp(-np.log(1e4) * np.arange(128) / 128.0)
+        assert np.abs(got - np.concatenate([np.cos(a64), np.sin(a64)])).max() <= 2e-4
+    # the model sees bf16(sigma): sigmas in one bf16 interval give the same embedding
+    assert np.array_equal(O.temb(0.8125), O.temb(0.81251))
+
+
+def test_conditioning_composition_matches_float64():
+    """Conditioning::compute (model.mm:582-590) as the oracle composes it, against numpy float64 with torch's
+    tanh-GELU: h = W1 e + b1, t = W2 gelu(h) + b2, tvec = Wp gelu(t) + bp."""
+    rng = np.random.default_rng(42)
+    D = 64
+    w1, w2, wp = (rng.standard_normal(s).astype(np.float32) / np.sqrt(s[0]) for s in ((256, D), (D, D), (D, 6 * D)))
+    b1, b2, bp = (0.1 * rng.standard_normal(n).astype(np.float32) for n in (D, D, 6 * D))
+    t, tvec = O.conditioning(0.6, w1, b1, w2, b2, wp, bp)
+    gelu = lambda v: torch.nn.functional.gelu(torch.from_numpy(v), approximate="tanh").numpy()  # noqa: E731
+    e = O.temb(0.6).astype(np.float64)
+    h = e @ w1 + b1
+    t64 = gelu(h) @ w2 + b2
+    tv64 = gelu(t64) @ wp + bp
+    assert rel_l2(t, t64) < 1e-5 and rel_l2(tvec, tv64) < 1e-5
+
+
+def test_make_fin_restatement():
+    """model.mm:340-346: fin = [nf (1 + t + lin0) ; t + lin1]; t = lin = 0 gives [nf ; 0]."""
+    rng = np.random.default_rng(43)
+    D = 96
+    t, nf = rng.standard_normal(D).astype(np.float32), rng.standard_normal(D).astype(np.float32)
+    lin = rng.standard_normal((2, D)).astype(np.float32)
+    f = O.make_fin(t, lin, nf)
+    assert np.array_equal(f[0], nf * ((np.float32(1) + t) + lin[0])) and np.array_equal(f[1], t + lin[1])
+    z = O.make_fin(np.zeros(D, np.float32), np.zeros((2, D), np.float32), nf)
+    assert np.array_equal(z[0], nf) and not z[1].any()
+
+
 def test_make_cond_special_cases():
     rng = np.random.default_rng(15)
     D = 64
