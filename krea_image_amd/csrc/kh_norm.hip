@@ -237,10 +237,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
         const int k = kb + u;
         if (k >= k1) break;
         float wv[CPL];
-        if (WF == 3) {
+        if constexpr (WF == 3) {
+          const f32x4 fv = __builtin_bit_cast(f32x4, raw[u]);
 #pragma unroll
-          for (int c = 0; c < 4; c++) wv[c] = __builtin_bit_cast(float, raw[u][c]);
-        } else if (WF == 0) {
+          for (int c = 0; c < 4; c++) wv[c] = fv[c];
+        } else if constexpr (WF == 0) {
 #pragma unroll
           for (int c = 0; c < 8; c++) {
             const uint16_t hb = (uint16_t)(raw[u][c >> 1] >> (16 * (c & 1)));
