@@ -93,6 +93,17 @@ size_t kh_gemm_workspace_bytes(void);
 /* Prepares a kh_gemm_ws workspace (a fill kernel on `stream`, so it may be captured in a graph). */
 int kh_gemm_workspace_init(kh_stream stream, void* workspace, size_t workspace_bytes, char* err, int errlen);
 
+/* kh_gemm_ws without a workspace argument and without any allocation: the stream-K workspace is a file-scope
+ * device array of the library (128 MiB + 16 KiB: one wave of up to 256 workgroups, what MI355X's 256 CUs use),
+ * which every GPU the library runs on holds until the process ends. No counterpart in the reference; for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops). Same arguments and
+ * results as kh_gemm_ws with a workspace (bitwise). Fails with KH_EINVAL, before any launch, on a device whose
+ * stream-K workspace would exceed the array (more than 256 CUs). The first call on a device clears the array's
+ * counters on `stream`. All calls on one GPU share its array: calls that may overlap in time on one GPU (other
+ * streams, other threads) race, so order them on one stream. */
+int kh_gemm_static(kh_stream stream, int epi, const void* A, int a_dtype, const kh_weight* W, void* C, int M, int N,
+                   int K, int lda, int ldw, int ldc, const void* vec, char* err, int errlen);
+
 /* Load-time rearrangement of int8 weights Wt[K, ldw] (row stride ldw bytes) into the packed layout kh_gemm reads
  * as w_dtype KH_I8P: element (k, n) at byte (k / 8) 8 ldw + 32 (n / 4) + 4 (k % 8) + n % 4, i.e. 8-row panels in
  * which each 4-column group's 8 x 4 bytes are contiguous. A GEMM thread loads one such group per K step (two

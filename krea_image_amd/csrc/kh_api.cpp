@@ -25,6 +25,14 @@ int kh_gemm_ws(kh_stream stream, int epi, const void* A, int a_dtype, const kh_w
 
 size_t kh_gemm_workspace_bytes(void) { return kh::gemm_workspace_bytes(); }
 
+int kh_gemm_static(kh_stream stream, int epi, const void* A, int a_dtype, const kh_weight* W, void* C, int M, int N,
+                   int K, int lda, int ldw, int ldc, const void* vec, char* err, int errlen) {
+  kh::Err e{err, errlen};
+  e.clear();
+  if (!W) return e.fail("gemm: null weight descriptor");
+  return kh::gemm_static((hipStream_t)stream, epi, A, a_dtype, *W, C, M, N, K, lda, ldw, ldc, vec, e);
+}
+
 int kh_gemm_workspace_init(kh_stream stream, void* workspace, size_t workspace_bytes, char* err, int errlen) {
   kh::Err e{err, errlen};
   e.clear();

@@ -251,6 +251,50 @@ int gemm_workspace_init(hipStream_t st, void* ws, size_t bytes, Err& e) {
   return r == hipSuccess ? KH_OK : e.hip(r, "gemm_workspace_init launch");
 }
 
+// ---- kh_gemm_static: kh_gemm_ws on a file-scope device array instead of a caller workspace, for callers that
+//      cannot allocate. The array holds the stream-K workspace of one wave of up to STATIC_CTAS workgroups. ----
+constexpr int STATIC_CTAS = 256;  // MI355X: 256 CUs
+constexpr size_t STATIC_SCRATCH_BYTES = (size_t)2 * STATIC_CTAS * BM * BN * sizeof(float) + SK_MAX_TILES * sizeof(int);
+static __device__ __align__(256) unsigned char scratch[STATIC_SCRATCH_BYTES];
+
+namespace {
+std::mutex scratch_mu;
+std::map<int, void*> scratch_ptr;  // device -> that device's copy of `scratch` (hipGetSymbolAddress)
+}  // namespace
+
+size_t gemm_static_scratch_bytes() { return STATIC_SCRATCH_BYTES; }
+
+int gemm_static(hipStream_t st, int epi, const void* A, int a_dtype, const kh_weight& W, void* C, int M, int N, int K,
+                int lda, int ldw, int ldc, const void* vec, Err& e) {
+  int dev = 0;
+  hipError_t r = hipGetDevice(&dev);
+  if (r != hipSuccess) return e.hip(r, "gemm_static: no device");
+  const size_t need = gemm_workspace_bytes_for(sk_cta_count(dev));
+  if (need > STATIC_SCRATCH_BYTES)
+    return e.fail("gemm_static: this device's stream-K workspace needs %zu bytes, the static scratch holds %zu", need,
+                  STATIC_SCRATCH_BYTES);
+  void* ptr = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(scratch_mu);
+    auto it = scratch_ptr.find(dev);
+    if (it != scratch_ptr.end()) {
+      ptr = it->second;
+    } else {
+      // first call on this device (it is current): the device address of its copy of the array; the host-side
+      // name `scratch` is not a device address and is never passed to a kernel
+      r = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+      if (r != hipSuccess) return e.hip(r, "gemm_static: hipGetSymbolAddress(scratch)");
+      // the counters start at zero (the array is zero-initialised at load; cleared again here so the contract
+      // does not rest on that), and every launch leaves them zero
+      const int rc = gemm_workspace_init(st, ptr, need, e);
+      if (rc) return rc;
+      scratch_ptr[dev] = ptr;
+    }
+  }
+  const GemmWs ws{ptr, need};
+  return gemm(st, epi, A, a_dtype, W, C, M, N, K, lda, ldw, ldc, vec, e, &ws);
+}
+
 int gemm_qk_norm_rope(hipStream_t st, const void* A, int a_dtype, const kh_weight& W, void* C, int M, int N, int K,
                       int lda, int ldw, int ldc, const QkNormRope& q, Err& e, const GemmWs* ws) {
   if (q.mode < 0 || q.mode > 2) return e.fail("gemm_qk_norm_rope: bad rope mode %d", q.mode);

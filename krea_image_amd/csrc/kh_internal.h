@@ -41,6 +41,10 @@ struct GemmWs {
 size_t gemm_workspace_bytes_for(int ctas);
 size_t gemm_workspace_bytes();  // for the current device
 int gemm_workspace_init(hipStream_t st, void* ws, size_t bytes, Err& e);
+// kh_gemm_ws with the library's static device scratch as the workspace (no allocation)
+int gemm_static(hipStream_t st, int epi, const void* A, int a_dtype, const kh_weight& W, void* C, int M, int N, int K,
+                int lda, int ldw, int ldc, const void* vec, Err& e);
+size_t gemm_static_scratch_bytes();
 
 int pack_int8(hipStream_t st, const void* W, int K, int ldw, void* out, Err& e);
 int gemm(hipStream_t st, int epi, const void* A, int a_dtype, const kh_weight& W, void* C, int M, int N, int K,
