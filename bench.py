@@ -9,10 +9,17 @@ synthetic and seed-generated on the device (no checkpoints). One step = one pass
 resident in HBM before the timed region. value = whole-job TFLOP/s = 2 * 618.48 GFLOP / step time.
 
 Reported beside it:
-  roofline     : the up-projection kernel (the dominant launch, 309.24 GFLOP, MFMA-bound), its average
-                 duration measured with HIP events on the launch stream, against 2.5 PFLOP/s dense fp16.
+  roofline     : the longer of the two launches in this run (the dominant kernel; both are 309.24 GFLOP and
+                 MFMA-bound), its average duration measured with HIP events on the launch stream, against
+                 2.5 PFLOP/s dense fp16; `roofline_kernels` carries the same figures for both launches.
+                 `traffic` is HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (scaled by a
+                 plain copy's reading), taken from the committed profile named in `traffic_source`: counters
+                 cannot be read inside this process.
   cpu_baseline : the CPU oracle (fp32 dequant + fp32 GEMM + the same epilogues, OpenMP) on this host, the full
-                 pair, median of 3 after one warm-up (rank 0, N = 1 only). A reported baseline, not a target.
+                 pair, median of 3 runs after one warm-up (rank 0, N = 1 only), on every core this process may
+                 use (its CPU affinity; OMP_NUM_THREADS caps it where set, as on the GPU boxes, whose share of
+                 the host is 16 cores); `nproc`, the affinity count and the CPU model are reported beside it.
+                 A reported baseline, not a target.
   dit_step_ms  : one full DiT denoising step at 1024^2 (4096 image + 512 text tokens, 71 blocks = 12.06 B
                  params of hidden 3072), the metric's second half (target < 500 ms).
   dit_step_reference : the same step on the reference architecture (hidden 6144, GQA 48/12, gated
@@ -41,9 +48,18 @@ M, D, FF = 4096, 3072, 12288
 PEAK_TFLOPS = 2500.0  # MI355X dense fp16 / bf16 MFMA
 FLOP_UP = 2.0 * M * D * FF
 FLOP_DOWN = 2.0 * M * FF * D
-# HBM bytes per up-projection launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, each scaled by the same
-# counter's reading for a 512 MiB copy (profiles/gemm_up_traffic_4096x3072x12288.md): 302.3 MB + 100.7 MB.
-UP_TRAFFIC_BYTES = 403.0e6
+# HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (KiB per dispatch), each scaled by the same
+# counter's reading for a 512 MiB copy (fetch x 2.000, write x 1.000). Source: TRAFFIC_SOURCE.
+TRAFFIC_SOURCE = "profiles/gemm_up_traffic_4096x3072x12288.md"
+TRAFFIC_BYTES = {
+    "up_gelu": (147621 * 2.0 + 98304 * 1.0) * 1024,    # 302.3 MB fetched + 100.7 MB written
+    "down_resid": (196705 * 2.0 + 49152 * 1.0) * 1024,  # 402.8 MB fetched + 50.3 MB written
+}
+KERNEL_NAMES = {
+    "up_gelu": "kh gemm_kernel<f16, int8 per-channel packed, GELU, 256x256 tiles> (up-projection, 309.24 GFLOP)",
+    "down_resid": "kh gemm_kernel<f16, int8 per-channel packed, f32 residual, 256x192 tiles> (down-projection, "
+                  "309.24 GFLOP)",
+}
 
 
 def make_inputs(dev, seed=1234):
@@ -155,11 +171,25 @@ def library_reference(dev, X, Wup, Wdown, H):
             "down_ms": round(down, 4), "down_tflops": round(FLOP_DOWN / down / 1e9, 1)}
 
 
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(X, x, Wup, Wdown):
-    """The CPU oracle on the same inputs (copied to the host), full pair, timed once."""
+    """The CPU oracle on the same inputs (copied to the host), full pair: median of 3 timed runs after one
+    warm-up, on every core this process may use (capped by OMP_NUM_THREADS where the environment sets it)."""
     import numpy as np
     from oracle import oracle as O
-    threads = min(os.cpu_count() or 1, 16)
+    affinity = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    threads = min(affinity, int(omp)) if omp.isdigit() and int(omp) > 0 else affinity
     A = X.cpu().view(torch.int16).numpy().view(np.uint16)
     qu, su = Wup.w.cpu().numpy(), Wup.s.cpu().view(torch.int16).numpy().view(np.uint16)
     qd, sd = Wdown.w.cpu().numpy(), Wdown.s.cpu().view(torch.int16).numpy().view(np.uint16)
@@ -176,7 +206,8 @@ def cpu_baseline(X, x, Wup, Wdown):
     times = sorted(run() for _ in range(3))
     dt = times[1]
     return {"value": round((FLOP_UP + FLOP_DOWN) / dt / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
-            "kind": "port", "seconds": round(dt, 3), "seconds_runs": [round(t, 3) for t in times],
+            "nproc": os.cpu_count(), "affinity_cores": affinity, "omp_num_threads": omp or None,
+            "cpu_model": _cpu_model(), "kind": "port", "seconds": round(dt, 3), "seconds_runs": [round(t, 3) for t in times],
             "sample": "the full MLP pair (4096 rows; up 3072->12288 + GELU, down 12288->3072 + residual), "
                       "fp32 dequant + fp32 GEMM, oracle/oracle.c with OpenMP; median of 3 after one warm-up"}
 
@@ -273,7 +304,14 @@ def main():
     down_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
 
     tflops = (FLOP_UP + FLOP_DOWN) / (ms_per_step * 1e-3) / 1e12
-    up_tflops = FLOP_UP / (up_ms * 1e-3) / 1e12
+    kms = {"up_gelu": up_ms, "down_resid": down_ms}
+
+    def roofline(k):
+        achieved = FLOP_UP / (kms[k] * 1e-3) / 1e12  # both launches are 309.24 GFLOP
+        return {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / PEAK_TFLOPS, 4), "traffic": round(TRAFFIC_BYTES[k]),
+                "traffic_source": TRAFFIC_SOURCE, "kernel": KERNEL_NAMES[k], "ms": round(kms[k], 4)}
+    dominant = max(kms, key=kms.get)
     out = {
         "metric": "dequant-GEMM TFLOP/s (% of MI355X MFMA peak); DiT step latency at 1024^2",
         "value": round(tflops, 2),
@@ -294,9 +332,8 @@ def main():
                    "parallelism": "single GPU"},
         "pct_of_peak": round(100 * tflops / PEAK_TFLOPS, 2),
         "kernels_ms": {"up_gelu": round(up_ms, 4), "down_resid": round(down_ms, 4)},
-        "roofline": {"bound": "mfma", "achieved": round(up_tflops, 2), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(up_tflops / PEAK_TFLOPS, 4), "traffic": UP_TRAFFIC_BYTES,
-                     "kernel": "kh gemm_kernel<f16, int8 per-channel packed, GELU> (up-projection, 309.24 GFLOP/launch)"},
+        "roofline": roofline(dominant),
+        "roofline_kernels": {k: roofline(k) for k in kms},
     }
     out["library_reference"] = library_reference(dev, X, Wup, Wdown, H)
     if not args.no_dit:
