@@ -69,7 +69,7 @@ def test_conditioning_fast_without_match_fails(dev, cond_file):
     from krea_image_amd import kh
     D = 256
     t, tvec = torch.empty(D, device=dev), torch.empty(6 * D, device=dev)
-    with pytest.raises(kh.KhError, match="4-step"):
+    with pytest.raises(kh.KhError, match="not in the fast schedule"):
         cond_file.conditioning(True, 0.55, t, tvec, torch.empty(256 + D, device=dev))
     with pytest.raises(kh.KhError, match="256 \\+ D"):
         cond_file.conditioning(False, 0.55, t, tvec, torch.empty(16, device=dev))
