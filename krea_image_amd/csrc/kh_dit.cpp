@@ -81,7 +81,6 @@ int dit_forward(hipStream_t st, const kh_dit_config& c, const kh_dit_layer* laye
   return KH_OK;
 }
 
-// engine/src/model.mm:290-315 (mode 0) and the 2-D variant of the benchmark configs (mode 1)
 // krea_sigmas (engine/src/model.mm:594-602)
 int sigmas(int steps, float mu, float* out) {
   if (steps <= 0 || !out) return KH_EINVAL;
@@ -93,6 +92,8 @@ int sigmas(int steps, float mu, float* out) {
   return KH_OK;
 }
 
+// RoPE tables of DiT::set_grid: engine/src/model.mm:290-315 (mode 0) and the 2-D variant of the benchmark
+// configs (mode 1)
 int rope_tables(int T, int H, int W, int mode, float* cosb, float* sinb) {
   if (T < 0 || H < 0 || W < 0 || (mode != 0 && mode != 1) || !cosb || !sinb) return KH_EINVAL;
   double om[64];
