@@ -291,7 +291,7 @@ int kh_qw_upload(kh_qw* f, kh_stream stream, char* err, int errlen);
 /* Timestep conditioning of one step: t [D] and tvec [6 D] (f32, device) for noise level sigma from an uploaded
  * cond.qw (tools/convert.py:287-308). Conditioning::get (engine/src/model.mm:545-569): a sigma equal to an
  * entry of the `base.` (fast = 0) or `fast.` (fast = 1) table copies that row; fast = 1 without a match fails
- * (KH_EINVAL, the reference's message). Otherwise Conditioning::compute (model.mm:571-591): e = [cos | sin](
+ * (KH_EINVAL: the fast schedule has no computed fallback, as in the reference). Otherwise Conditioning::compute (model.mm:571-591): e = [cos | sin](
  * bf16(sigma) 1000 10000^(-i/128)), i < 128, on the host; then on the device h = tmlp1(e), t = tmlp2(gelu(h)),
  * tvec = tproj(gelu(t)) as f32 GEMVs (kh_gemv, GELU on load). work: device f32 scratch of >= 256 + D floats
  * (unused on a table hit). *from_table (may be NULL) = 1 on a table hit, else 0. Stream-ordered. */
