@@ -122,3 +122,45 @@ def compile_to_asm(src, out, include_dir, hipcc="/opt/rocm/bin/hipcc"):
            "-packed-fp32-ops", "--cuda-device-only", "-S", "-I", include_dir, "-o", out, src]
     subprocess.run(cmd, check=True, capture_output=True)
     return open(out).read()
+
+
+def loop_depth_blocks(body):
+    """[(label, loop depth, [instructions])] of one kernel's assembly, the depth read from the compiler's
+    loop comments on each block label (`in Loop: ... Depth=d`, `Inner Loop Header: Depth=d`; 0 if none)."""
+    out, lines = [], body.split("\n")
+    for idx, raw in enumerate(lines):
+        m = re.match(r"(\.LBB\w+|; %bb\.\d+):(.*)", raw)
+        if m:
+            depths = [int(d) for d in re.findall(r"Depth=(\d+)", m.group(2))]
+            k = idx + 1
+            while k < len(lines) and lines[k].strip().startswith(";"):  # continuation comment lines
+                depths += [int(d) for d in re.findall(r"Depth=(\d+)", lines[k])]
+                k += 1
+            out.append((m.group(1), max(depths, default=0), []))
+            continue
+        line = raw.split(";")[0].strip()
+        if out and line and not line.startswith(".") and not line.endswith(":"):
+            out[-1][2].append(line)
+    return out
+
+
+def scratch_in_inner_mfma_loop(body):
+    """Scratch (spill) accesses in the deepest loop that holds MFMAs: the K loop of a GEMM tile."""
+    blocks = loop_depth_blocks(body)
+    mfma_depths = [d for _, d, ins in blocks if any(i.startswith("v_mfma") for i in ins)]
+    if not mfma_depths or max(mfma_depths) == 0:
+        return []
+    top = max(mfma_depths)
+    return [(lab, i) for lab, d, ins in blocks if d == top for i in ins if i.startswith("scratch_")]
+
+
+def kernel_spills(text, name_filter):
+    """{kernel symbol: (vgpr spill count, private segment bytes)} from the code-object metadata."""
+    res = {}
+    for block in re.split(r"\n\s+- \.", text):
+        n = re.search(r"\.name:\s+(\S+)", block)
+        s = re.search(r"\.vgpr_spill_count:\s+(\d+)", block)
+        p = re.search(r"\.private_segment_fixed_size:\s+(\d+)", block)
+        if n and s and p and name_filter in n.group(1):
+            res[n.group(1)] = (int(s.group(1)), int(p.group(1)))
+    return res
