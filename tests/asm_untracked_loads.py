@@ -125,33 +125,42 @@ def compile_to_asm(src, out, include_dir, hipcc="/opt/rocm/bin/hipcc"):
 
 
 def loop_depth_blocks(body):
-    """[(label, loop depth, [instructions])] of one kernel's assembly, the depth read from the compiler's
-    loop comments on each block label (`in Loop: ... Depth=d`, `Inner Loop Header: Depth=d`; 0 if none)."""
+    """[(label, loop depth, loop header, [instructions])] of one kernel's assembly, read from the compiler's
+    loop comments on each block label (`in Loop: Header=BBx Depth=d`, `Inner Loop Header: Depth=d`; a
+    loop header is its own loop's header; depth 0 and no header outside loops)."""
     out, lines = [], body.split("\n")
     for idx, raw in enumerate(lines):
         m = re.match(r"(\.LBB\w+|; %bb\.\d+):(.*)", raw)
         if m:
-            depths = [int(d) for d in re.findall(r"Depth=(\d+)", m.group(2))]
+            notes = [m.group(2)]
             k = idx + 1
             while k < len(lines) and lines[k].strip().startswith(";"):  # continuation comment lines
-                depths += [int(d) for d in re.findall(r"Depth=(\d+)", lines[k])]
+                notes.append(lines[k])
                 k += 1
-            out.append((m.group(1), max(depths, default=0), []))
+            note = " ".join(notes)
+            depths = [int(d) for d in re.findall(r"Depth=(\d+)", note)]
+            if "Loop Header" in note:
+                header = m.group(1).lstrip(".L")
+            else:
+                h = re.search(r"in Loop: Header=(BB\w+)", note)
+                header = h.group(1) if h else None
+            out.append((m.group(1), max(depths, default=0), header, []))
             continue
         line = raw.split(";")[0].strip()
         if out and line and not line.startswith(".") and not line.endswith(":"):
-            out[-1][2].append(line)
+            out[-1][3].append(line)
     return out
 
 
 def scratch_in_inner_mfma_loop(body):
-    """Scratch (spill) accesses in the deepest loop that holds MFMAs: the K loop of a GEMM tile."""
+    """Scratch (spill) accesses in the innermost loops that hold MFMAs: the K loop of a GEMM tile."""
     blocks = loop_depth_blocks(body)
-    mfma_depths = [d for _, d, ins in blocks if any(i.startswith("v_mfma") for i in ins)]
-    if not mfma_depths or max(mfma_depths) == 0:
+    mfma = [(d, h) for _, d, h, ins in blocks if any(i.startswith("v_mfma") for i in ins)]
+    if not mfma or max(d for d, _ in mfma) == 0:
         return []
-    top = max(mfma_depths)
-    return [(lab, i) for lab, d, ins in blocks if d == top for i in ins if i.startswith("scratch_")]
+    top = max(d for d, _ in mfma)
+    loops = {h for d, h in mfma if d == top}
+    return [(lab, i) for lab, d, h, ins in blocks if d == top and h in loops for i in ins if i.startswith("scratch_")]
 
 
 def kernel_spills(text, name_filter):

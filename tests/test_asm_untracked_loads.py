@@ -56,10 +56,9 @@ def test_gemm_kernels_have_no_untracked_load_hazards(tmp_path, unit):
     assert len(res) >= 80, f"expected every GEMM instantiation, found {len(res)}"
     bad = {k: v[:3] for k, v in res.items() if v}
     assert not bad, f"inline-asm load destinations used before their wait: {bad}"
-    # Register budget: no spill traffic inside the K loop (the deepest loop holding MFMAs) of any
-    # int8-weight instantiation. Known exceptions: 16-bit-weight (WF_16) stream-K kernels at 256-wide tiles
-    # (the VAE conv among them) reload one or two spilled dwords per two K steps; the count is capped so a
-    # new one cannot slip in.
+    # Register budget: no spill traffic inside the K loop (the innermost loop holding MFMAs) of any
+    # int8-weight instantiation. Known exceptions: three 16-bit-weight (WF_16) stream-K kernels at 256-wide
+    # tiles reload one or two spilled dwords per two K steps; the count is capped so a new one cannot slip in.
     loop_spills = {}
     for f in re.split(r"\n(?=_ZN\S*:)", text):
         name = f.split(":", 1)[0]
@@ -67,9 +66,9 @@ def test_gemm_kernels_have_no_untracked_load_hazards(tmp_path, unit):
             hits = scratch_in_inner_mfma_loop(f[:f.find(".Lfunc_end")])
             if hits:
                 loop_spills[name] = hits
-    unexpected = [k for k in loop_spills if not re.search(r"gemm_kernelILi\d+ELi0ELi\d+ELi8ELb1ELi256ELb[01]E", k)]
+    unexpected = [k for k in loop_spills if not re.search(r"gemm_kernelILi\d+ELi0ELi\d+ELi8ELb1ELi256ELb0E", k)]
     assert not unexpected, f"scratch accesses inside a GEMM K loop: {unexpected}"
-    assert len(loop_spills) <= 4, f"more 16-bit-weight stream-K kernels spill in the K loop: {sorted(loop_spills)}"
+    assert len(loop_spills) <= 3, f"more 16-bit-weight stream-K kernels spill in the K loop: {sorted(loop_spills)}"
 
 
 @pytest.mark.skipif(not os.path.exists("/opt/rocm/bin/hipcc"), reason="hipcc not available")
