@@ -143,3 +143,36 @@ def test_conditioning_and_make_fin_reject_null(lib):
     rc = lib.kh_conditioning(None, None, 0, ctypes.c_float(0.5), p, p, p, 4096, None, err, 256)
     assert rc == -1 and "null" in err.value.decode()
     assert lib.kh_make_fin(None, None, p, p, 64, p, err, 256) == -1
+
+
+def _attn_call(lib, **kw):
+    from krea_image_amd import kh
+    a = dict(Q=16, K=16, V=16, O=16, dtype=kh.F16, Lq=64, Lk=64, heads=2, ldq=256, ldk=256, ldv=256, ldo=256,
+             group=1, causal=0, q_pos0=0, G=None, ldg=0, QB=None, KB=None)
+    a.update(kw)
+    err = ctypes.create_string_buffer(256)
+    vp = lambda x: None if x is None else ctypes.c_void_p(x)
+    rc = lib.kh_attention(None, vp(a["Q"]), vp(a["K"]), vp(a["V"]), vp(a["O"]), a["dtype"], a["Lq"], a["Lk"],
+                          a["heads"], a["ldq"], a["ldk"], a["ldv"], a["ldo"], a["group"], a["causal"], a["q_pos0"],
+                          vp(a["G"]), a["ldg"], vp(a["QB"]), vp(a["KB"]), err, 256)
+    return rc, err.value.decode()
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(dtype=0), "dtype"),
+    (dict(Lk=0), "empty"),
+    (dict(heads=3, group=2), "multiple of group"),
+    (dict(K=None), "null"),
+    (dict(ldq=128), "row strides"),
+    (dict(ldk=260), "16-byte rows"),
+    (dict(Q=24), "16-byte aligned"),
+    (dict(O=20), "8-byte aligned"),
+    (dict(G=16, ldg=128), "gate"),
+    (dict(QB=16), "go together"),
+    (dict(Lk=1 << 24, ldk=256), "too large"),
+])
+def test_attention_rejects_without_launch(lib, kw, msg):
+    """Metal::attention's shape and layout contract (engine/src/metal.mm:193-202), checked on the host before
+    any launch: fake device pointers never reach a kernel."""
+    rc, text = _attn_call(lib, **kw)
+    assert rc == -1 and msg in text, (rc, text)
