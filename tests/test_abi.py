@@ -176,3 +176,48 @@ def test_attention_rejects_without_launch(lib, kw, msg):
     any launch: fake device pointers never reach a kernel."""
     rc, text = _attn_call(lib, **kw)
     assert rc == -1 and msg in text, (rc, text)
+
+
+def test_norms_and_f32_gemm_reject_without_launch(lib):
+    """rms_norm / qk_norm_rope (engine/src/metal.mm:174-191) and gemm_f32 (metal.mm:165-172) check their
+    arguments on the host; fake device pointers never reach a kernel."""
+    from krea_image_amd import kh
+    err = ctypes.create_string_buffer(256)
+    p = ctypes.c_void_p(16)
+
+    def rms(**kw):
+        a = dict(x=p, mul=p, add=None, y=p, dt=kh.F16, rows=4, width=64, ld_in=64, ld_out=64)
+        a.update(kw)
+        return lib.kh_rms_norm(None, a["x"], a["mul"], a["add"], a["y"], a["dt"], a["rows"], a["width"],
+                               a["ld_in"], a["ld_out"], 1e-6, 0, err, 256), err.value.decode()
+
+    for kw, msg in [(dict(rows=0), "empty"), (dict(width=66, ld_in=66, ld_out=66), "unsupported"),
+                    (dict(width=8196, ld_in=8196, ld_out=8196), "unsupported"), (dict(mul=None), "null"),
+                    (dict(dt=kh.I8), "out dtype")]:
+        rc, text = rms(**kw)
+        assert rc == -1 and msg in text, (kw, text)
+
+    def qknr(**kw):
+        a = dict(qkv=p, dt=kh.F16, wq=p, wk=p, cos=p, sin=p, rows=4, ld=768, q_off=0, n_q=2, k_off=256, n_k=2,
+                 mode=0, big=-1, qbig=None, kbig=None)
+        a.update(kw)
+        return lib.kh_qk_norm_rope(None, a["qkv"], a["dt"], a["wq"], a["wk"], a["cos"], a["sin"], a["rows"], a["ld"],
+                                   a["q_off"], a["n_q"], a["k_off"], a["n_k"], 1e-5, a["mode"], a["big"], a["qbig"],
+                                   a["kbig"], err, 256), err.value.decode()
+
+    for kw, msg in [(dict(dt=kh.F32), "dtype"), (dict(n_q=0, n_k=0), "empty"), (dict(mode=3), "rope mode"),
+                    (dict(cos=None), "cos / sin"), (dict(wk=None), "null"), (dict(big=5), "big_dim"),
+                    (dict(ld=769), "even"), (dict(k_off=260), "16-byte"),
+                    (dict(qkv=ctypes.c_void_p(24)), "16-byte")]:
+        rc, text = qknr(**kw)
+        assert rc == -1 and msg in text, (kw, text)
+
+    def gf32(**kw):
+        a = dict(A=p, W=p, C=p, M=4, N=8, K=8, lda=8, ldw=8, ldc=8, mode=0, bias=None)
+        a.update(kw)
+        return lib.kh_gemm_f32(None, a["A"], a["W"], a["C"], a["M"], a["N"], a["K"], a["lda"], a["ldw"], a["ldc"],
+                               a["mode"], a["bias"], err, 256), err.value.decode()
+
+    for kw, msg in [(dict(M=0), "empty"), (dict(mode=1), "bias"), (dict(W=None), "null"), (dict(ldc=4), "strides")]:
+        rc, text = gf32(**kw)
+        assert rc == -1 and msg in text, (kw, text)
