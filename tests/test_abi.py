@@ -221,3 +221,28 @@ def test_norms_and_f32_gemm_reject_without_launch(lib):
     for kw, msg in [(dict(M=0), "empty"), (dict(mode=1), "bias"), (dict(W=None), "null"), (dict(ldc=4), "strides")]:
         rc, text = gf32(**kw)
         assert rc == -1 and msg in text, (kw, text)
+
+
+@pytest.mark.parametrize("kw,rows,n,msg", [
+    (dict(dim=200), 4, 1, "heads * 128"),
+    (dict(kv_heads=3), 4, 1, "kv_heads"),
+    (dict(ff=100), 4, 1, "ff must"),
+    (dict(mlp=2), 4, 1, "mlp must"),
+    (dict(dtype=0), 4, 1, "dtype"),
+    (dict(), 0, 1, "rows"),
+    (dict(), 4, -1, "layer list"),
+    (dict(), 4, 1, "missing state buffer"),
+])
+def test_dit_forward_rejects_without_launch(lib, kw, rows, n, msg):
+    """DiT::run_layers (engine/src/model.mm:519-525) through kh_dit_forward: the block configuration, the
+    row count, the layer list and the state buffers are checked before the first launch."""
+    from krea_image_amd import kh
+    c = dict(dim=256, heads=2, kv_heads=2, ff=512, mlp=0, attn_gate=0, norm_center=0, rope_mode=0,
+             dtype=kh.F16, eps=1e-6)
+    c.update(kw)
+    cfg = kh.DitConfig(**c)
+    layers = (kh.DitLayerC * 1)()
+    state = kh.DitStateC()
+    err = ctypes.create_string_buffer(256)
+    rc = lib.kh_dit_forward(None, ctypes.byref(cfg), layers, n, ctypes.byref(state), rows, err, 256)
+    assert rc == -1 and msg in err.value.decode(), (rc, err.value)
