@@ -246,3 +246,23 @@ def test_dit_forward_rejects_without_launch(lib, kw, rows, n, msg):
     err = ctypes.create_string_buffer(256)
     rc = lib.kh_dit_forward(None, ctypes.byref(cfg), layers, n, ctypes.byref(state), rows, err, 256)
     assert rc == -1 and msg in err.value.decode(), (rc, err.value)
+
+
+def test_vae_decode_rejects_without_launch(lib):
+    """VAEDecoder::run (engine/src/vae.mm:289-337) through kh_vae_decode: null operands, latent sizes outside
+    1..512, a short or misaligned workspace are refused before any launch."""
+    from krea_image_amd import vae
+    vae._bind(lib)
+    vp = ctypes.c_void_p
+    need = lib.kh_vae_workspace_bytes(64, 64)
+    assert need > 0 and lib.kh_vae_workspace_bytes(0, 64) == 0
+    assert lib.kh_vae_workspace_bytes(64, 64) < lib.kh_vae_workspace_bytes(64, 128)
+    err = ctypes.create_string_buffer(256)
+    p = vp(256)
+    cases = [(dict(f=None), "null"), (dict(h=0), "out of range"), (dict(w=513), "out of range"),
+             (dict(ws_bytes=need - 1), "workspace"), (dict(ws=vp(264)), "256-byte aligned")]
+    for kw, msg in cases:
+        a = dict(f=p, z=p, h=64, w=64, ws=p, ws_bytes=need, rgba=p)
+        a.update(kw)
+        rc = lib.kh_vae_decode(None, a["f"], a["z"], a["h"], a["w"], a["ws"], a["ws_bytes"], a["rgba"], err, 256)
+        assert rc == -1 and msg in err.value.decode(), (kw, err.value)
