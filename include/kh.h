@@ -90,6 +90,12 @@ int kh_gemm_ws(kh_stream stream, int epi, const void* A, int a_dtype, const kh_w
                int errlen);
 /* Workspace size kh_gemm_ws uses on the current device (0 if no device). */
 size_t kh_gemm_workspace_bytes(void);
+/* The launch kh_gemm (with_ws 0) or kh_gemm_ws with a full workspace (with_ws 1) makes for an M x N x K GEMM on a
+ * device with `ctas` CUs (a positive multiple of 8), computed on the host without a device: out[0] = tile width
+ * (256, 192, or 128 for 16-bit weights, w16 = 1), out[1] = workgroups, out[2] = K steps per workgroup (0: one
+ * tile per workgroup, data-parallel; > 0: stream-K). No counterpart in the reference, whose Metal::gemm grid is
+ * fixed (engine/src/metal.mm:146-163); for tests and for schedulers that size work per launch. */
+int kh_gemm_plan(int M, int N, int K, int epi, int w16, int ctas, int with_ws, int* out, char* err, int errlen);
 /* Prepares a kh_gemm_ws workspace (a fill kernel on `stream`, so it may be captured in a graph). */
 int kh_gemm_workspace_init(kh_stream stream, void* workspace, size_t workspace_bytes, char* err, int errlen);
 

@@ -25,6 +25,12 @@ int kh_gemm_ws(kh_stream stream, int epi, const void* A, int a_dtype, const kh_w
 
 size_t kh_gemm_workspace_bytes(void) { return kh::gemm_workspace_bytes(); }
 
+int kh_gemm_plan(int M, int N, int K, int epi, int w16, int ctas, int with_ws, int* out, char* err, int errlen) {
+  kh::Err e{err, errlen};
+  e.clear();
+  return kh::gemm_plan(M, N, K, epi, w16, ctas, with_ws, out, e);
+}
+
 int kh_gemm_static(kh_stream stream, int epi, const void* A, int a_dtype, const kh_weight* W, void* C, int M, int N,
                    int K, int lda, int ldw, int ldc, const void* vec, char* err, int errlen) {
   kh::Err e{err, errlen};

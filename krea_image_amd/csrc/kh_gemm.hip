@@ -58,12 +58,12 @@ bool narrow_enabled() {
 // under 60 % of their last wave and 256-wide stream-K needs less work per CU (padded width x tiles / CUs
 // against waves x width).
 // tn_div > 0: the tile width must divide tn_div (sub-pixel convs: a tile may not straddle two phases).
-void plan_launch(GemmArgs& a, int epi, const GemmWs* ws, int& grid_x, int& tn, bool narrow128 = false, int tn_div = 0) {
+// ctas: workgroups of one full wave on the device (one per CU, a multiple of 8; 0 if unknown).
+void plan_launch_for(GemmArgs& a, int epi, const GemmWs* ws, int ctas, int& grid_x, int& tn, bool narrow128,
+                     int tn_div) {
   const int tiles_m = (a.M + BM - 1) / BM;
   const int nk = a.K / BK;
   auto padded = [&](int w) { return (a.N + w - 1) / w * w; };
-  int dev = 0;
-  const int ctas = hipGetDevice(&dev) == hipSuccess ? sk_cta_count(dev) : 0;
   tn = BN;
   if (tn_div > 0) {
     tn = tn_div % BN == 0 ? BN : tn_div % 192 == 0 ? 192 : 128;
@@ -111,7 +111,31 @@ void plan_launch(GemmArgs& a, int epi, const GemmWs* ws, int& grid_x, int& tn, b
   }
 }
 
+// plan_launch_for on the current device
+void plan_launch(GemmArgs& a, int epi, const GemmWs* ws, int& grid_x, int& tn, bool narrow128 = false, int tn_div = 0) {
+  int dev = 0;
+  const int ctas = hipGetDevice(&dev) == hipSuccess ? sk_cta_count(dev) : 0;
+  plan_launch_for(a, epi, ws, ctas, grid_x, tn, narrow128, tn_div);
+}
+
 }  // namespace
+
+// The launch kh_gemm / kh_gemm_ws would make for this shape on a device with `ctas` CUs, without a device:
+// out = {tile width, workgroups, K steps per workgroup (0: data-parallel)}.
+int gemm_plan(int M, int N, int K, int epi, int w16, int ctas, int with_ws, int* out, Err& e) {
+  if (epi < KH_EPI_STORE16 || epi > KH_EPI_BIAS_F32) return e.fail("gemm_plan: unknown epilogue %d", epi);
+  if (M <= 0 || N <= 0 || K <= 0 || N % 64 || K % BK) return e.fail("gemm_plan: unsupported shape");
+  if (ctas <= 0 || ctas % 8) return e.fail("gemm_plan: ctas=%d must be a positive multiple of 8", ctas);
+  if (!out) return e.fail("gemm_plan: null out");
+  GemmArgs a{nullptr, nullptr, nullptr, nullptr, nullptr, M, N, K, K, N, N, 0, KH_F32, 0, nullptr, nullptr};
+  const GemmWs ws{(void*)(uintptr_t)256, gemm_workspace_bytes_for(ctas)};  // never dereferenced
+  int grid_x = 0, tn = BN;
+  plan_launch_for(a, epi, with_ws ? &ws : nullptr, ctas, grid_x, tn, w16 != 0, 0);
+  out[0] = tn;
+  out[1] = grid_x;
+  out[2] = a.sk_iters;
+  return KH_OK;
+}
 
 namespace {
 

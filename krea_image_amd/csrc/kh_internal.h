@@ -39,6 +39,7 @@ struct GemmWs {
   size_t bytes;
 };
 size_t gemm_workspace_bytes_for(int ctas);
+int gemm_plan(int M, int N, int K, int epi, int w16, int ctas, int with_ws, int* out, Err& e);
 size_t gemm_workspace_bytes();  // for the current device
 int gemm_workspace_init(hipStream_t st, void* ws, size_t bytes, Err& e);
 // kh_gemm_ws with the library's static device scratch as the workspace (no allocation)

@@ -34,7 +34,8 @@ SYMBOLS = ["kh_version", "kh_gemm", "kh_attention", "kh_rms_norm", "kh_qk_norm_r
            "kh_upload", "kh_download", "kh_vae_conv3x3", "kh_vae_subpix_weights", "kh_vae_conv_up2", "kh_vae_im2col", "kh_vae_norm_silu", "kh_vae_unpack", "kh_vae_softmax",
            "kh_vae_conv_out", "kh_vae_workspace_bytes", "kh_vae_decode", "kh_gemm_qk_norm_rope",
            "kh_pack_int8", "kh_sigmas", "kh_euler_step", "kh_cfg_combine", "kh_copy", "kh_make_fin", "kh_conditioning",
-           "kh_gemm_ws", "kh_gemm_workspace_bytes", "kh_gemm_workspace_init", "kh_gemm_static"]
+           "kh_gemm_ws", "kh_gemm_workspace_bytes", "kh_gemm_workspace_init", "kh_gemm_static",
+           "kh_gemm_plan"]
 
 
 class KhError(RuntimeError):
@@ -90,6 +91,8 @@ def load():
                                        ctypes.c_char_p, i]
         lib.kh_gemm_static.restype = i
         lib.kh_gemm_workspace_bytes.argtypes, lib.kh_gemm_workspace_bytes.restype = [], ctypes.c_size_t
+        lib.kh_gemm_plan.argtypes = [i, i, i, i, i, i, i, ctypes.POINTER(ctypes.c_int), ctypes.c_char_p, i]
+        lib.kh_gemm_plan.restype = i
         lib.kh_gemm_workspace_init.argtypes = [vp, vp, ctypes.c_size_t, ctypes.c_char_p, i]
         lib.kh_gemm_workspace_init.restype = i
         lib.kh_attention.argtypes = [vp, vp, vp, vp, vp, i, i, i, i, i, i, i, i, i, i, i, vp, i, vp, vp,

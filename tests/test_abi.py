@@ -266,3 +266,43 @@ def test_vae_decode_rejects_without_launch(lib):
         a.update(kw)
         rc = lib.kh_vae_decode(None, a["f"], a["z"], a["h"], a["w"], a["ws"], a["ws_bytes"], a["rgba"], err, 256)
         assert rc == -1 and msg in err.value.decode(), (kw, err.value)
+
+
+def _plan(lib, M, N, K, epi, w16=0, ctas=256, with_ws=1):
+    out = (ctypes.c_int * 3)()
+    err = ctypes.create_string_buffer(256)
+    rc = lib.kh_gemm_plan(M, N, K, epi, w16, ctas, with_ws, out, err, 256)
+    assert rc == 0, err.value
+    return tuple(out)
+
+
+@pytest.mark.parametrize("M,N,K,epi,w16,with_ws,want", [
+    # MLP up-projection at 1024^2: 768 tiles of 256 x 256 fill three waves exactly
+    (4096, 12288, 3072, 5, 0, 1, (256, 768, 0)),
+    # down-projection: 192 wide tiles fill the one wave (256 tiles) that 256-wide ones leave 25 % idle
+    (4096, 3072, 12288, 2, 0, 1, (192, 256, 0)),
+    # 1536 rows (1024^2 at 512 text + 1024 image tokens): 288 tiles = 56 % of two waves -> stream-K
+    (1536, 12288, 3072, 5, 0, 1, (256, 256, 288 * 48 // 256)),
+    # the same without a workspace stays data-parallel
+    (1536, 12288, 3072, 5, 0, 0, (256, 288, 0)),
+    # 4608 rows x 12288: 864 tiles (84 % of four waves): data-parallel on 256-wide tiles (192-wide measured slower)
+    (4608, 12288, 3072, 5, 0, 1, (256, 864, 0)),
+    # 4608 x 3072 x 3072: 216 tiles fill 84 % of one wave; stream-K measured slower (140 vs 103 us)
+    (4608, 3072, 3072, 6, 0, 1, (256, 216, 0)),
+    # SwiGLU keeps 256-wide tiles (its 64-column gate | up interleave)
+    (4096, 2 * 8192 + 192, 3072, 4, 0, 1, (256, 16 * 65, 0)),
+    # 16-bit weights, N = 128: 128-wide tiles pad least
+    (65536, 128, 384, 6, 1, 1, (128, 256, 0)),
+])
+def test_gemm_plan_pins_measured_launch_choices(lib, M, N, K, epi, w16, with_ws, want):
+    """The launch planner's choices at the shapes its thresholds were measured on (256 CUs): tile width,
+    workgroups, and K steps per workgroup for stream-K."""
+    assert _plan(lib, M, N, K, epi, w16, 256, with_ws) == want
+
+
+def test_gemm_plan_rejects(lib):
+    err = ctypes.create_string_buffer(256)
+    out = (ctypes.c_int * 3)()
+    assert lib.kh_gemm_plan(64, 64, 64, 0, 0, 100, 1, out, err, 256) == -1 and "multiple of 8" in err.value.decode()
+    assert lib.kh_gemm_plan(64, 96, 64, 0, 0, 256, 1, out, err, 256) == -1 and "shape" in err.value.decode()
+    assert lib.kh_gemm_plan(64, 64, 64, 9, 0, 256, 1, out, err, 256) == -1 and "epilogue" in err.value.decode()
