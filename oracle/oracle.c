@@ -15,8 +15,10 @@
  *   or_gemv                 numpy fp64 matvec; torch silu / gelu(approximate="tanh") for the on-load activations.
  *   or_temb                 closed forms: sigma = 0 gives cos = 1, sin = 0; numpy float64 of the same formula
  *                           at bf16(sigma) (<= 1e-5 absolute); bf16 rounding of sigma checked against torch.
- *   or_make_fin             numpy restatement of model.mm:340-346 on random vectors.
- *   or_make_cond            numpy restatement of model.mm:329-338 on random vectors.
+ *   or_make_fin             unit impulses in t and in each lin row: each moves only the fin entries that
+ *                           model.mm:340-346 names, by nf[k] or 1 (a lin row swap or dropped term fails).
+ *   or_make_cond            unit impulses at tvec[j*D+k] (and the table): exactly mods[j][k] moves, by n1[k],
+ *                           n2[k] or 1 (model.mm:329-338; row meaning from DiT::layer, model.mm:374-382).
  *   or_rms_norm             numpy fp64; torch layer_norm for center = 1.
  *   or_qk_norm_rope         complex-multiplication form of RoPE (numpy); rotate-half vs pairs equivalence
  *                           under a channel permutation; norm of every head preserved by the rotation.

@@ -296,6 +296,54 @@ def test_make_cond_special_cases():
     assert not m[0].any() and not m[3].any()
 
 
+def test_make_cond_one_hot_rows():
+    """model.mm:329-338, pinned row by row. DiT::layer (model.mm:374-382) consumes mods row 0 as the first norm's
+    multiplier, row 1 as its additive shift, row 2 as the attention gate, rows 3/4/5 likewise for the MLP half.
+    A unit impulse at tvec[j*D+k] must move exactly mods[j][k]: by n1[k] (j = 0), n2[k] (j = 3) or 1 (otherwise);
+    any swap of rows (shift/gate, v4/v5) or of n1/n2 fails here."""
+    rng = np.random.default_rng(151)
+    D = 48
+    n1 = (1.5 + rng.random(D)).astype(np.float32)       # distinct from 1 and from each other
+    n2 = (-3.0 - rng.random(D)).astype(np.float32)
+    base = O.make_cond(np.zeros(6 * D, np.float32), None, n1, n2)
+    for j in range(6):
+        for k in (0, 7, D - 1):
+            tv = np.zeros(6 * D, np.float32)
+            tv[j * D + k] = 1.0
+            d = O.make_cond(tv, None, n1, n2) - base
+            want = np.zeros((6, D), np.float32)
+            want[j, k] = n1[k] if j == 0 else n2[k] if j == 3 else 1.0
+            assert np.array_equal(d, want), (j, k)
+            # the per-layer table enters exactly where tvec does
+            dt = O.make_cond(np.zeros(6 * D, np.float32), tv, n1, n2) - base
+            assert np.array_equal(dt, want), ("table", j, k)
+
+
+def test_make_fin_one_hot_rows():
+    """model.mm:340-346 pinned by impulses: t[k] moves fin[0][k] by nf[k] and fin[1][k] by 1; lin row 0 moves only
+    fin[0][k] (by nf[k]); lin row 1 moves only fin[1][k] (by 1). A lin row swap or a dropped t term fails."""
+    rng = np.random.default_rng(152)
+    D = 40
+    nf = (2.0 + rng.random(D)).astype(np.float32)
+    z = np.zeros(D, np.float32)
+    base = O.make_fin(z, np.zeros((2, D), np.float32), nf)
+    assert np.array_equal(base[0], nf) and not base[1].any()
+    for k in (0, 11, D - 1):
+        t = z.copy()
+        t[k] = 1.0
+        d = O.make_fin(t, np.zeros((2, D), np.float32), nf) - base
+        want = np.zeros((2, D), np.float32)
+        want[0, k], want[1, k] = nf[k], 1.0
+        assert np.array_equal(d, want), ("t", k)
+        for r in (0, 1):
+            lin = np.zeros((2, D), np.float32)
+            lin[r, k] = 1.0
+            d = O.make_fin(z, lin, nf) - base
+            want = np.zeros((2, D), np.float32)
+            want[r, k] = nf[k] if r == 0 else 1.0
+            assert np.array_equal(d, want), ("lin", r, k)
+
+
 # ---------------------------------------------------------------------------------------------- norms, RoPE
 @pytest.mark.parametrize("center", [0, 1])
 def test_rms_and_layer_norm_match_torch(center):
