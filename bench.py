@@ -182,40 +182,6 @@ def _cpu_model():
     return "unknown"
 
 
-def mfma_sustained(dev, iters=400):
-    """Sustained v_mfma_f32_32x32x16_f16 rate of this GPU (krea_image_amd/libkh_probe.so): 4 workgroups of 8
-    waves per CU, 32 MFMAs per wave and iteration on register operands, (a) the same operands for every
-    MFMA and (b) random fp16 operands whose mantissas flip every iteration. Context for the roofline: the
-    rate the chip holds under the data-dependent power of real operands, against the 2.5 PFLOP/s spec."""
-    import ctypes
-    lib = ctypes.CDLL(os.path.join(ROOT, "krea_image_amd", "libkh_probe.so"))
-    lib.kh_probe_mfma_rate.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                       ctypes.c_int, ctypes.c_void_p]
-    cus = torch.cuda.get_device_properties(dev).multi_processor_count
-    n_slots, grid = cus, 4 * cus
-    g = torch.Generator(device=dev)
-    g.manual_seed(11)
-    mag = torch.rand(n_slots * 512 * 8 * 8, generator=g, device=dev) * 1.5 + 0.5  # |x| in [0.5, 2)
-    sign = torch.randint(0, 2, mag.shape, generator=g, device=dev) * 2 - 1
-    rand_ops = (mag * sign).half()
-    const_ops = torch.full_like(rand_ops, 0.75)
-    sink = torch.zeros(512, device=dev)
-    stream = torch.cuda.current_stream()
-    out = {}
-    for name, ops, vary in (("const_operands", const_ops, 0), ("random_operands", rand_ops, 1)):
-        def launch():
-            rc = lib.kh_probe_mfma_rate(ctypes.c_void_p(stream.cuda_stream), ctypes.c_void_p(ops.data_ptr()), n_slots,
-                                        grid, iters, vary, ctypes.c_void_p(sink.data_ptr()))
-            if rc != 0:
-                raise RuntimeError(f"kh_probe_mfma_rate failed: hipError {rc}")
-        ms = _event_ms(launch, 3, warm=1)
-        flop = 2.0 * 32 * 32 * 16 * 32 * iters * 8 * grid
-        out[name] = round(flop / ms / 1e9, 1)
-    out["unit"] = "TFLOP/s"
-    out["probe"] = "krea_image_amd/csrc/probe/kh_probe.hip"
-    return out
-
-
 def cpu_baseline(X, x, Wup, Wdown):
     """The CPU oracle on the same inputs (copied to the host), full pair: median of 3 timed runs after one
     warm-up, on every core this process may use (capped by OMP_NUM_THREADS where the environment sets it)."""
@@ -253,14 +219,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-dit", action="store_true", help="skip the full DiT step latency")
-    ap.add_argument("--probe", nargs="?", const="gemm", choices=["gemm", "attention", "dit", "dit_ref", "vae", "peak"],
+    ap.add_argument("--probe", nargs="?", const="gemm", choices=["gemm", "attention", "dit", "dit_ref", "vae"],
                     help="profiling probe, no JSON line: 'gemm' = one up-projection launch and one 512 MiB device "
                          "copy (for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE calibration); 'attention' = three "
                          "launches of the joint attention of config [2] (4608 tokens x 24 heads, fp16); 'dit' = two full "
                          "DiT steps at 1024^2 (71 blocks); 'dit_ref' = two reference-architecture steps (28 blocks); "
                          "'vae' = the VAE decode of a 64 x 64 "
-                         "latent (1024^2 RGBA), 2 + 5 calls; 'peak' = the sustained MFMA rate with constant and "
-                         "random operands (JSON)")
+                         "latent (1024^2 RGBA), 2 + 5 calls")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the dequant-GEMM path has no multi-GPU mode in this build "
@@ -294,9 +259,6 @@ def main():
     if args.probe == "dit_ref":
         from krea_image_amd import dit
         dit.bench_step(dev, rows_img=4096, rows_txt=512, shape=dit.reference_shape(28), steps=2)
-        return
-    if args.probe == "peak":
-        print(json.dumps(mfma_sustained(dev)), flush=True)
         return
     if args.probe == "vae":
         print(json.dumps(vae_decode_bench(dev)), flush=True)

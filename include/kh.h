@@ -101,12 +101,13 @@ int kh_gemm_workspace_init(kh_stream stream, void* workspace, size_t workspace_b
 
 /* kh_gemm_ws without a workspace argument and without any allocation: the stream-K workspace is a file-scope
  * device array of the library (128 MiB + 16 KiB: one wave of up to 256 workgroups, what MI355X's 256 CUs use),
- * which every GPU the library runs on holds until the process ends. No counterpart in the reference; for callers
- * that cannot allocate device memory (code under HIP graph capture, tight serving loops). Same arguments and
- * results as kh_gemm_ws with a workspace (bitwise). Fails with KH_EINVAL, before any launch, on a device whose
- * stream-K workspace would exceed the array (more than 256 CUs). The first call on a device clears the array's
- * counters on `stream`. All calls on one GPU share its array: calls that may overlap in time on one GPU (other
- * streams, other threads) race, so order them on one stream. */
+ * which every GPU the library runs on holds until the process ends, whether or not this entry point is called.
+ * No counterpart in the reference; for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops). Same arguments and results as kh_gemm_ws with a workspace (bitwise). A device whose
+ * stream-K workspace would exceed the array (more than 256 CUs) runs every shape data-parallel, as kh_gemm_ws
+ * does with a short workspace. The first call on a device, outside graph capture, clears the array's counters on
+ * `stream` and waits for that stream. All calls on one GPU share its array: calls that may overlap in time on one
+ * GPU (other streams, other threads) race, so order them on one stream. */
 int kh_gemm_static(kh_stream stream, int epi, const void* A, int a_dtype, const kh_weight* W, void* C, int M, int N,
                    int K, int lda, int ldw, int ldc, const void* vec, char* err, int errlen);
 
@@ -300,7 +301,8 @@ int kh_qw_upload(kh_qw* f, kh_stream stream, char* err, int errlen);
  * (KH_EINVAL: the fast schedule has no computed fallback, as in the reference). Otherwise Conditioning::compute (model.mm:571-591): e = [cos | sin](
  * bf16(sigma) 1000 10000^(-i/128)), i < 128, on the host; then on the device h = tmlp1(e), t = tmlp2(gelu(h)),
  * tvec = tproj(gelu(t)) as f32 GEMVs (kh_gemv, GELU on load). work: device f32 scratch of >= 256 + D floats
- * (unused on a table hit). *from_table (may be NULL) = 1 on a table hit, else 0. Stream-ordered. */
+ * (unused on a table hit, may be NULL then). A table hit reads only the table tensors (D from `<pre>t`), so a
+ * file holding just the tables serves the sigmas they list. *from_table (may be NULL) = 1 on a table hit, else 0. Stream-ordered. */
 int kh_conditioning(kh_stream stream, const kh_qw* cond, int fast, float sigma, float* t, float* tvec, float* work,
                     size_t work_bytes, int* from_table, char* err, int errlen);
 

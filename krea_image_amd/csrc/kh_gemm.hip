@@ -294,9 +294,9 @@ int gemm_static(hipStream_t st, int epi, const void* A, int a_dtype, const kh_we
   hipError_t r = hipGetDevice(&dev);
   if (r != hipSuccess) return e.hip(r, "gemm_static: no device");
   const size_t need = gemm_workspace_bytes_for(sk_cta_count(dev));
-  if (need > STATIC_SCRATCH_BYTES)
-    return e.fail("gemm_static: this device's stream-K workspace needs %zu bytes, the static scratch holds %zu", need,
-                  STATIC_SCRATCH_BYTES);
+  // a device whose stream-K workspace is larger than the array (more than STATIC_CTAS CUs) runs every shape
+  // data-parallel, as kh_gemm_ws does with a NULL or short workspace
+  if (need > STATIC_SCRATCH_BYTES) return gemm(st, epi, A, a_dtype, W, C, M, N, K, lda, ldw, ldc, vec, e, nullptr);
   void* ptr = nullptr;
   {
     std::lock_guard<std::mutex> lk(scratch_mu);
@@ -308,10 +308,19 @@ int gemm_static(hipStream_t st, int epi, const void* A, int a_dtype, const kh_we
       // name `scratch` is not a device address and is never passed to a kernel
       r = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
       if (r != hipSuccess) return e.hip(r, "gemm_static: hipGetSymbolAddress(scratch)");
-      // the counters start at zero (the array is zero-initialised at load; cleared again here so the contract
-      // does not rest on that), and every launch leaves them zero
-      const int rc = gemm_workspace_init(st, ptr, need, e);
-      if (rc) return rc;
+      // The counters start at zero: the array is zero-initialised when the code object loads, and every launch
+      // leaves them zero. Outside graph capture they are cleared once more and the stream is waited on, so
+      // that a first call on another stream cannot overtake the clear. Under capture neither is possible
+      // (the fill would be replayed; a wait is illegal) and the load-time zeros stand.
+      hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+      r = hipStreamIsCapturing(st, &cs);
+      if (r != hipSuccess) return e.hip(r, "gemm_static: hipStreamIsCapturing");
+      if (cs == hipStreamCaptureStatusNone) {
+        const int rc = gemm_workspace_init(st, ptr, need, e);
+        if (rc) return rc;
+        r = hipStreamSynchronize(st);
+        if (r != hipSuccess) return e.hip(r, "gemm_static: clearing the scratch counters");
+      }
       scratch_ptr[dev] = ptr;
     }
   }

@@ -200,6 +200,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
   constexpr int OUT = RMAX * COLS;                    // partial sums per k-group
   constexpr int TPO = 256 / OUT;                      // threads per output in the final reduction
   __shared__ float part[GEMV_KG][OUT + 1];
+  // gfx950 gives a workgroup up to 160 KiB of LDS; the int8 four-row form uses 128 x 129 x 4 = 66,048 bytes
+  // (two workgroups per CU), above the 64 KiB of earlier CDNA parts, so this kernel is gfx950-only as sized
+  static_assert(sizeof(part) <= 160 * 1024, "gemv_kernel: partial sums exceed the 160 KiB LDS of a gfx950 CU");
+  static_assert(256 % OUT == 0 && GEMV_KG % (256 / OUT) == 0, "gemv_kernel: outputs must split the workgroup");
   const int tid = threadIdx.x, li = tid & 1, kg = tid >> 1;
   const int nblk = gridDim.x;
   const int b = nblk % 8 == 0 ? (int)(blockIdx.x & 7) * (nblk >> 3) + (int)(blockIdx.x >> 3) : (int)blockIdx.x;

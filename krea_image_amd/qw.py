@@ -394,11 +394,12 @@ class QwFile:
     def conditioning(self, fast: bool, sigma: float, t, tvec, work) -> bool:
         """kh_conditioning on this (uploaded) cond.qw: t [D] and tvec [6 D] (f32 device tensors) for noise level
         sigma, Conditioning::get / compute (engine/src/model.mm:545-591); work: f32 device scratch of >= 256 + D
-        floats. Returns True when the sigma was found in the schedule's table."""
+        floats (None is enough for a table hit). Returns True when the sigma was found in the schedule's table."""
         hit = ctypes.c_int(0)
         err = ctypes.create_string_buffer(512)
+        wp, wb = (None, 0) if work is None else (kh._ptr(work), work.numel() * work.element_size())
         rc = kh.load().kh_conditioning(kh._stream(), self.h, int(fast), float(sigma), kh._ptr(t), kh._ptr(tvec),
-                                       kh._ptr(work), work.numel() * work.element_size(), ctypes.byref(hit), err, 512)
+                                       wp, wb, ctypes.byref(hit), err, 512)
         kh._check(rc, err)
         return bool(hit.value)
 

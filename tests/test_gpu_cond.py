@@ -75,6 +75,35 @@ def test_conditioning_fast_without_match_fails(dev, cond_file):
         cond_file.conditioning(False, 0.55, t, tvec, torch.empty(16, device=dev))
 
 
+def test_conditioning_tables_only_file(dev, tmp_path):
+    """Conditioning::get reads only the schedule tables (model.mm:545-569): a cond file holding just the tables
+    serves a listed sigma (bitwise row copy, D from the table's shape) and reports a missing MLP on a miss."""
+    from krea_image_amd import kh, qw
+    D = 128
+    rng = np.random.default_rng(22)
+    specs = [sp for sp in qw.cond_specs(D, len(BASE), len(FAST)) if sp[0].startswith(("base.", "fast."))]
+    path = str(tmp_path / "tables.qw")
+    w = qw.QwWriter(path, specs, {"model": "tables-only"})
+    rows = {}
+    for tag, sig in (("base", BASE), ("fast", FAST)):
+        w.write(tag + ".sigma", np.asarray(sig, np.float32))
+        rows[tag] = (rng.standard_normal((len(sig), D), dtype=np.float32),
+                     rng.standard_normal((len(sig), 6 * D), dtype=np.float32))
+        w.write(tag + ".t", rows[tag][0])
+        w.write(tag + ".tvec", rows[tag][1])
+    w.close()
+    print("[conditioning tables-only]", flush=True)
+    with qw.QwFile(path) as f:
+        f.upload()
+        t, tvec = torch.empty(D, device=dev), torch.empty(6 * D, device=dev)
+        assert f.conditioning(True, float(np.float32(FAST[1])), t, tvec, None)
+        torch.cuda.synchronize()
+        assert np.array_equal(t.cpu().numpy(), rows["fast"][0][1])
+        assert np.array_equal(tvec.cpu().numpy(), rows["fast"][1][1])
+        with pytest.raises(kh.KhError, match="tmlp1.w"):
+            f.conditioning(False, 0.55, t, tvec, torch.empty(256 + D, device=dev))
+
+
 def test_make_fin(dev):
     from krea_image_amd import kh
     rng = np.random.default_rng(4)
