@@ -45,6 +45,13 @@ int sk_cta_count(int dev) {
 
 size_t sk_part_bytes(int ctas) { return (size_t)2 * ctas * BM * BN * sizeof(float); }
 
+// KH_GEMM_WAHEAD=3 loads weights three K steps ahead in the instantiations that have that form (has_wa3);
+// unset or 2: two steps (read per call)
+int wa_choice() {
+  const char* e = getenv("KH_GEMM_WAHEAD");
+  return e && e[0] == '3' && e[1] == 0 ? 3 : 2;
+}
+
 // KH_GEMM_TN192=0 keeps every data-parallel launch on 256-wide tiles (read per call)
 bool narrow_enabled() {
   const char* e = getenv("KH_GEMM_TN192");
@@ -199,6 +206,7 @@ int gemm_run(hipStream_t st, int epi, const void* A, int a_dtype, const kh_weigh
   int grid_x = 0, tn = BN;
   if (ws && ws->p && ((uintptr_t)ws->p & 255)) return e.fail("gemm: workspace must be 256-byte aligned");
   plan_launch(a, epi, ws, grid_x, tn, wf == WF_16);
+  a.wa = wa_choice();
   hipError_t r = a_dtype == KH_F16 ? launch_gemm_f16(wf, epi, a, grid_x, tn, st)
                                    : launch_gemm_bf16(wf, epi, a, grid_x, tn, st);
   if (r != hipSuccess) return e.hip(r, "gemm launch");

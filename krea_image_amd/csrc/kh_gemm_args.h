@@ -58,7 +58,16 @@ struct GemmArgs {
   float *qk_qbig, *qk_kbig;
   int qk_qoff, qk_nq, qk_koff, qk_nk, qk_mode, qk_big;
   float qk_eps;
+  // host-side launch choice, not read by the kernel: K steps ahead that weights are loaded (2, or 3 for the
+  // instantiations that have the three-set form; see gemm_kernel's WA)
+  int wa = 2;
 };
+// the weight formats / tile widths with a three-step weight prefetch instantiation (WA = 3): packed int8 with
+// per-channel scales, data-parallel; 256-wide tiles only with fp16 activations (the bf16 conversion needs
+// the registers the third set would take)
+constexpr bool has_wa3(int act, int wf, int tn) {
+  return wf == (WF_I8_CHANNEL | WF_PK) && (tn != 256 || act == KH_F16);
+}
 
 // launch the GEMM kernel instantiation for (activation type, weight format wf, epilogue epi, tile width tn):
 // kh_gemm_f16.hip / kh_gemm_bf16.hip

@@ -159,10 +159,16 @@ struct Cfg {
 // tiles of 192 instead of 16 x 12). The waves' n extent is TN / 2 = JB blocks of 32.
 // CONV: the activation tile is gathered from an image as an implicit 3 x 3 convolution (GemmArgs cv_*).
 // WFX: weight format, optionally | WF_PK (packed int8 layout).
-template <int ACT, int WFX, int EPI, int WAVES, bool SK, int TN = BN, bool CONV = false>
+// WA: K steps ahead that weights are loaded (2 or 3). With 2, the loads issued in step t (activations and
+// weights of step t + 2) are waited for at the start of step t + 1: each has one step to land. With 3, the
+// weights of step t + 3 go into a third raw register set and the step waits once, at its end, for the loads
+// issued one step earlier: activations and weights both get two steps. The same products are summed in the
+// same order: results are bitwise equal.
+template <int ACT, int WFX, int EPI, int WAVES, bool SK, int TN = BN, bool CONV = false, int WA = 2>
 __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
   constexpr bool PK = (WFX & WF_PK) != 0;
   constexpr int WF = WFX & ~WF_PK;
+  static_assert(WA == 2 || (WA == 3 && !SK && !CONV), "three-step weight prefetch: data-parallel GEMMs only");
   static_assert(!PK || (WF != WF_16 && !CONV), "packed layout: int8 weights, plain GEMM");
   using C_ = Cfg<WAVES>;
   static_assert(TN == BN || ((TN == 192 || TN == 128) && !SK && !wide_only(EPI)),
@@ -384,6 +390,31 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
     lds_barrier();  // this step's converted weights and (waited above) step t + 1's activations are visible
   };
 
+  // WA = 3: multiply stage t; convert raw(t + 1) (Rc, retired at the end of step t - 1) into the other W stage;
+  // issue the activations of step t + 2 and the weights of step t + 3 (into Rl); at the end wait for what step
+  // t - 1 issued (activations of t + 1, weights of t + 2 in Rn) and tie Rn to that wait.
+  auto step3 = [&](int t, WRaw<WF, KR>& Rc, WRaw<WF, KR>& Rn, WRaw<WF, KR>& Rl) {
+    issue_x_to(min(t + 2, ns - 1), (t + 2) % X_STAGES);
+    issue_w(min(t + 3, ns - 1), Rl);
+    const char* xs = lds + (t % X_STAGES) * STAGE;
+    const char* ws = lds + (X_STAGES + (t & 1)) * STAGE;
+    u32x4 wf[2][JB], xf[2][IB];
+    read_frags(xs, ws, 0, wf[0], xf[0]);
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+      if (s < 3) read_frags(xs, ws, s + 1, wf[(s + 1) & 1], xf[(s + 1) & 1]);
+      SCHED_FENCE();
+#pragma unroll
+      for (int jb = 0; jb < JB; jb++)
+#pragma unroll
+        for (int ib = 0; ib < IB; ib++) acc[jb][ib] = mfma32<ACT>(wf[s & 1][jb], xf[s & 1][ib], acc[jb][ib]);
+      store_w(Rc, (t + 1) & 1, s);
+      SCHED_FENCE();
+    }
+    ready_w(Rn, NewerT{});  // step t - 1's group has landed: activations of t + 1 in LDS, weights of t + 2
+    lds_barrier();
+  };
+
   bool first_seg = true;
   if (it < it_end) for (;;) {  // segments; uniform: every thread walks the same ones (one when !SK)
   const int tile = it / nk;
@@ -402,6 +433,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
 #pragma unroll
     for (int ib = 0; ib < IB; ib++) acc[jb][ib] = (f32x16){};
 
+  if constexpr (WA == 2) {
   WRaw<WF, KR> R0, R1;
   issue_x_to(0, 0);
   issue_w(0, R0);
@@ -422,6 +454,34 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
   // other values while the (untracked) loads are still in flight and the loads would overwrite them.
   ready_w(R0, std::integral_constant<int, 0>{});
   ready_w(R1, std::integral_constant<int, 0>{});
+  } else {
+  // groups in issue order: {X(0), W(0), W(1)}, {X(1), W(2)}; the first is waited for (the second, LOADS
+  // loads, may stay in flight), then step t issues {X(t + 2), W(t + 3)} and retires {X(t + 1), W(t + 2)}
+  WRaw<WF, KR> R0, R1, R2;
+  issue_x_to(0, 0);
+  issue_w(0, R0);
+  issue_w(min(1, ns - 1), R1);
+  issue_x_to(min(1, ns - 1), 1);
+  issue_w(min(2, ns - 1), R2);
+  ready_w(R0, NewerT{});
+  ready_w(R1, NewerT{});
+#pragma unroll
+  for (int q = 0; q < 4; q++) store_w(R0, 0, q);
+  lds_barrier();
+  int t = 0;
+  for (; t + 2 < ns; t += 3) {
+    step3(t, R1, R2, R0);
+    step3(t + 1, R2, R0, R1);
+    step3(t + 2, R0, R1, R2);
+  }
+  if (t < ns) {  // nested: the second remainder step converts R2, which only the first one's wait retires
+    step3(t, R1, R2, R0);
+    if (t + 1 < ns) step3(t + 1, R2, R0, R1);
+  }
+  ready_w(R0, std::integral_constant<int, 0>{});
+  ready_w(R1, std::integral_constant<int, 0>{});
+  ready_w(R2, std::integral_constant<int, 0>{});
+  }
   lds_barrier();
 
   // ---- stream-K: a tile split over workgroups c0..c1 (K order). Each stores its partial accumulators to
@@ -693,6 +753,17 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
   }  // segments
 }
 
+template <int ACT, int WF, int E, int TN, bool CONV>
+void launch_dp(const GemmArgs& a, const dim3& grid, const dim3& block, hipStream_t st) {
+  if constexpr (!CONV && has_wa3(ACT, WF, TN)) {
+    if (a.wa == 3) {
+      hipLaunchKernelGGL((gemm_kernel<ACT, WF, E, WAVES_DEFAULT, false, TN, CONV, 3>), grid, block, 0, st, a);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((gemm_kernel<ACT, WF, E, WAVES_DEFAULT, false, TN, CONV>), grid, block, 0, st, a);
+}
+
 template <int ACT, int WF, int E, bool CONV = false>
 void launch_one(const GemmArgs& a, int grid_x, int tn, hipStream_t st) {
   const dim3 grid(grid_x), block(64 * WAVES_DEFAULT);
@@ -702,17 +773,17 @@ void launch_one(const GemmArgs& a, int grid_x, int tn, hipStream_t st) {
   }
   if constexpr (!wide_only(E)) {
     if (tn == 192) {
-      hipLaunchKernelGGL((gemm_kernel<ACT, WF, E, WAVES_DEFAULT, false, 192, CONV>), grid, block, 0, st, a);
+      launch_dp<ACT, WF, E, 192, CONV>(a, grid, block, st);
       return;
     }
     if constexpr (WF == WF_16) {  // 128-wide tiles: 16-bit weights only (the VAE's narrow channel counts)
       if (tn == 128) {
-        hipLaunchKernelGGL((gemm_kernel<ACT, WF, E, WAVES_DEFAULT, false, 128, CONV>), grid, block, 0, st, a);
+        launch_dp<ACT, WF, E, 128, CONV>(a, grid, block, st);
         return;
       }
     }
   }
-  hipLaunchKernelGGL((gemm_kernel<ACT, WF, E, WAVES_DEFAULT, false, BN, CONV>), grid, block, 0, st, a);
+  launch_dp<ACT, WF, E, BN, CONV>(a, grid, block, st);
 }
 
 template <int ACT, int WF>
