@@ -21,7 +21,9 @@ Reported beside it:
                  the host is 16 cores); `nproc`, the affinity count and the CPU model are reported beside it.
                  A reported baseline, not a target.
   dit_step_ms  : one full DiT denoising step at 1024^2 (4096 image + 512 text tokens, 71 blocks = 12.06 B
-                 params of hidden 3072), the metric's second half (target < 500 ms).
+                 params of hidden 3072), the metric's second half (target < 500 ms), launched eagerly;
+                 `dit_step.graph_ms` is the same step replayed from a HIP graph (`graph_equal`: its output is
+                 bitwise the eager one's).
   dit_step_reference : the same step on the reference architecture (hidden 6144, GQA 48/12, gated
                  attention, SwiGLU, 28 blocks, group-128 int8), a secondary line.
   library_reference : torch.matmul (hipBLASLt) on the same two shapes with fp16 weights and no epilogue,
@@ -338,7 +340,7 @@ def main():
     out["library_reference"] = library_reference(dev, X, Wup, Wdown, H)
     if not args.no_dit:
         from krea_image_amd import dit
-        step_info = dit.bench_step(dev, rows_img=4096, rows_txt=512, layers=71)
+        step_info = dit.bench_step(dev, rows_img=4096, rows_txt=512, layers=71, graph=True)
         out["dit_step_ms"] = step_info["ms"]
         out["dit_step"] = dict(step_info, workload="one full denoising step at 1024^2: 4096 image + 512 text "
                                "tokens, 71 blocks of hidden 3072 / 24 heads / MLP x4 (12.06 B params, int8 "

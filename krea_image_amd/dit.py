@@ -212,6 +212,21 @@ class DitRunner:
         kh.gemm_f32(self.hf, self.last_w, vel, M, C, D, D, C, C, 1, self.last_b)
         return vel
 
+    def capture(self, txt: torch.Tensor, z: torch.Tensor, vel: torch.Tensor) -> torch.cuda.CUDAGraph:
+        """forward(txt, z, vel) recorded once into a HIP graph (torch.cuda.CUDAGraph on a default-priority capture
+        stream): replay() re-runs the whole step (embed, every layer's ~9 launches, head) as one graph launch on
+        the same tensors, whose contents may change between replays. Every op the step enqueues is a kernel (no
+        memset or allocation inside: the stream-K counters are cleared by the kernels themselves), so the graph
+        holds kernel nodes and torch's copy only. The launches are the same as eager forward's: results are
+        bitwise equal."""
+        self.forward(txt, z, vel)  # first launches (lazy loading of kernels) outside the capture
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.forward(txt, z, vel)
+        torch.cuda.synchronize()
+        return g
+
     def denoise(self, txt: torch.Tensor, z: torch.Tensor, sig, vel: Optional[torch.Tensor] = None,
                 before_step=None, neg: Optional["DitRunner"] = None, ntxt: Optional[torch.Tensor] = None,
                 cfg_scale: float = 0.0):
@@ -316,9 +331,10 @@ class QwDit(DitRunner):
 
 
 def bench_step(dev, rows_img: int = 4096, rows_txt: int = 512, layers: int = 71, steps: int = 3,
-               shape: Optional[DitShape] = None, grid: Optional[tuple] = None) -> dict:
+               shape: Optional[DitShape] = None, grid: Optional[tuple] = None, graph: bool = False) -> dict:
     """Latency of one full denoising step (embed + all layers + head) at the given token count; the image
-    tokens form an H x W latent grid (square by default)."""
+    tokens form an H x W latent grid (square by default). graph=True also times the step replayed from a HIP
+    graph (DitRunner.capture): `graph_ms`, the same launches without the host's per-launch gaps."""
     shape = shape or baseline_shape(layers)
     if grid is None:
         side = int(round(rows_img ** 0.5))
@@ -341,6 +357,28 @@ def bench_step(dev, rows_img: int = 4096, rows_txt: int = 512, layers: int = 71,
     flop = shape.layers * shape.flop_per_layer(run.R)
     out = {"ms": round(ms, 3), "layers": shape.layers, "rows": run.R, "dim": shape.dim,
            "tflops": round(flop / (ms * 1e-3) / 1e12, 1), "finite": bool(torch.isfinite(vel).all().item())}
+    if graph:
+        try:
+            g = run.capture(txt, z, vel)
+        except RuntimeError as ex:  # a capture the runtime refuses leaves the eager figure standing
+            out["graph_error"] = str(ex)[:200]
+            graph = False
+    if graph:
+        # the replayed step must equal the eager one (the graph holds the same launches)
+        ref = vel.clone()
+        g.replay()
+        torch.cuda.synchronize()
+        out["graph_equal"] = bool(torch.equal(ref, vel))
+        g.replay()  # warm-up
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            g.replay()
+        torch.cuda.synchronize()
+        gms = (time.perf_counter() - t0) * 1e3 / steps
+        out["graph_ms"] = round(gms, 3)
+        out["graph_tflops"] = round(flop / (gms * 1e-3) / 1e12, 1)
+        del g
     del run
     torch.cuda.empty_cache()
     return out
