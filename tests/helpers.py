@@ -34,6 +34,8 @@ def make_weight(rng, K, N, kind, a_dtype):
     """Synthetic weight in one of the three formats (numpy side):
     'ch'  : int8 U{-127..127} [K, N] + fp16 per-output-channel scales |N(0, 0.02)| / 127 (benchmark configs)
     'g128': convert.py q8 of W ~ N(0, 0.02): int8 [K, N] + f32 scales [K/128, N] (reference dit_q8 format)
+    'g64h' / 'g256b': the same quantizer with groups of 64 / 256 rows, scales stored as fp16 / bf16
+    'chf32' / 'chbf': int8 + per-output-channel scales stored as f32 / bf16
     '16'  : W ~ N(0, 0.02) as 16-bit [K, N]
     Returns dict(w=np array, s=np array or None, w_dtype, s_dtype, group)."""
     if kind == "ch":
@@ -44,6 +46,19 @@ def make_weight(rng, K, N, kind, a_dtype):
         w = rng.standard_normal((K, N)).astype(np.float32) * np.float32(0.02)
         q, s = O.quant_q8(w, 128)
         return dict(w=q, s=s, w_dtype=O.I8, s_dtype=O.F32, group=128)
+    if kind in ("g64h", "g256b"):
+        # other groups, scales stored as fp16 / bf16 (kh_weight s_dtype KH_F16 / KH_BF16 with group < K)
+        group, s_dt = (64, O.F16) if kind == "g64h" else (256, O.BF16)
+        w = rng.standard_normal((K, N)).astype(np.float32) * np.float32(0.02)
+        q, s = O.quant_q8(w, group)
+        return dict(w=q, s=O.from_f32(s, s_dt), w_dtype=O.I8, s_dtype=s_dt, group=group)
+    if kind in ("chf32", "chbf"):
+        # per-output-channel scales stored as f32 / bf16
+        q = rng.integers(-127, 128, size=(K, N), dtype=np.int8)
+        s = np.abs(rng.standard_normal(N).astype(np.float32) * np.float32(0.02)) / np.float32(127)
+        if kind == "chf32":
+            return dict(w=q, s=s, w_dtype=O.I8, s_dtype=O.F32, group=K)
+        return dict(w=q, s=O.from_f32(s, O.BF16), w_dtype=O.I8, s_dtype=O.BF16, group=K)
     w = rng.standard_normal((K, N)).astype(np.float32) * np.float32(0.02)
     return dict(w=O.from_f32(w, a_dtype), s=None, w_dtype=a_dtype, s_dtype=O.F32, group=0)
 

@@ -53,6 +53,19 @@ def test_attention_ragged(dev, Lq, Lk):
     run(dev, O.F16, Lq, Lk, 2, seed=Lq + Lk)
 
 
+@pytest.mark.parametrize("dtype,heads,group", [(O.F16, 4, 4), (O.BF16, 8, 8)])
+def test_attention_mqa(dev, dtype, heads, group):
+    """One K / V head shared by every query head (group = heads)."""
+    run(dev, dtype, 150, 333, heads, group=group, gate=True, seed=11)
+
+
+@pytest.mark.parametrize("Lq,Lk", [(1, 4608), (3, 4096), (64, 4097)])
+def test_attention_few_queries_many_keys(dev, Lq, Lk):
+    """A handful of queries over a long key range (one partly filled workgroup, 64 .. 73 key blocks, a ragged
+    last block)."""
+    run(dev, O.BF16, Lq, Lk, 2, seed=Lq + Lk)
+
+
 def test_attention_gqa_gate(dev):
     run(dev, O.BF16, 192, 320, 8, group=4, gate=True, seed=3)
 

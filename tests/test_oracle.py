@@ -125,6 +125,22 @@ def test_gemm_golden_group128_bf16():
     assert K == 256
 
 
+@pytest.mark.parametrize("kind", ["g64h", "g256b", "chf32", "chbf"])
+@pytest.mark.parametrize("a_dtype", [O.F16, O.BF16])
+def test_gemm_fp64_brute_force_scale_formats(kind, a_dtype):
+    """The other scale storage formats (fp16 / bf16 group scales at groups 64 and 256; per-channel f32 / bf16)
+    against the float64 restatement: per-channel scales multiply the exact integer sum, group scales dequantize
+    each weight once (q s in f32, rounded to the activation type; gemm.metal:190-196)."""
+    from tests.helpers import make_weight
+    rng = np.random.default_rng(19)
+    M, K, N = 21, 512, 192
+    A = O.from_f32(rng.standard_normal((M, K)).astype(np.float32), a_dtype)
+    wd = make_weight(rng, K, N, kind, a_dtype)
+    got = O.gemm(O.EPI["f32"], A, a_dtype, wd["w"], wd["w_dtype"], wd["s"], wd["s_dtype"], wd["group"])
+    ref = _acc64(A, a_dtype, wd["w"], wd["w_dtype"], wd["s"], wd["s_dtype"], wd["group"])
+    assert rel_l2(got, ref) < 1e-6
+
+
 @pytest.mark.parametrize("kind", ["ch", "g128", "16"])
 @pytest.mark.parametrize("a_dtype", [O.F16, O.BF16])
 def test_gemm_fp64_brute_force(kind, a_dtype):
