@@ -116,6 +116,41 @@ def test_gemv(dev, kind, act, rows):
     assert rel_l2(outs[0].numpy(), ref) < 1e-5
 
 
+@pytest.mark.parametrize("kind", ["g64h", "f16", "chbf"])
+@pytest.mark.parametrize("rows", [2, 4])
+def test_gemv_ragged(dev, kind, rows):
+    """kh_gemv on the shapes the sweep above leaves out: 2 and 4 rows (the four-row instantiation), fp16 weights,
+    fp16 group scales (groups of 64) and bf16 per-channel scales, K that is not a multiple of the 128-way K split
+    (uneven split, a short last range) and N that leaves the last workgroup's second lane group past the end."""
+    from krea_image_amd import kh
+    rng = np.random.default_rng(500 + rows)
+    if kind == "g64h":
+        K, N = 960, 1040
+        w, s32 = O.quant_q8((rng.standard_normal((K, N)) * 0.02).astype(np.float32), 64)
+        s = O.from_f32(s32, O.F16)
+        W = kh.Weight(torch.from_numpy(w).to(dev), to_dev16(s, O.F16, dev), 64)
+        wargs = (w, O.I8, s, O.F16, 64)
+    elif kind == "chbf":
+        K, N = 1000, 1040
+        w = rng.integers(-127, 128, (K, N), dtype=np.int8)
+        s = O.from_f32(np.abs(rng.standard_normal(N)).astype(np.float32) * 1e-4, O.BF16)
+        W = kh.Weight(torch.from_numpy(w).to(dev), to_dev16(s, O.BF16, dev), K)
+        wargs = (w, O.I8, s, O.BF16, K)
+    else:
+        K, N = 1000, 1032
+        w = O.from_f32((rng.standard_normal((K, N)) * 0.02).astype(np.float32), O.F16)
+        W = kh.Weight(to_dev16(w, O.F16, dev))
+        wargs = (w, O.F16, None, O.F32, 0)
+    print(f"[gemv ragged] {kind} rows={rows} K={K} N={N}", flush=True)
+    x = rng.standard_normal((rows, K)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    y = torch.zeros(rows, N, device=dev)
+    kh.gemv(torch.from_numpy(x).to(dev), W, y, rows, N, K, N, 4, torch.from_numpy(bias).to(dev))
+    torch.cuda.synchronize()
+    ref = O.gemv(x, *wargs, y=np.zeros((rows, N), np.float32), act=4, bias=bias)
+    assert rel_l2(y.cpu().numpy(), ref) < 1e-5
+
+
 def test_gemv_rejects_bad_act(dev):
     from krea_image_amd import kh
     W = kh.Weight(torch.zeros(64, 64, device=dev))
