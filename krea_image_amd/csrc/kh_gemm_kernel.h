@@ -179,7 +179,10 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
   __shared__ __attribute__((aligned(1024))) char lds[(X_STAGES + W_STAGES) * STAGE];
   typedef __attribute__((address_space(3))) void lds_void;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // WA = 3 also reads the wave index into a scalar, so wave-uniform values (the LDS DMA destinations in M0,
+  // panel offsets) stay on the scalar unit (the two-step instantiations keep their per-lane form)
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = WA == 3 ? __builtin_amdgcn_readfirstlane(tid >> 6) : tid >> 6;
 
   // ---- work of this workgroup: a range of K steps over the tile sequence. Data-parallel: one whole tile.
   //      Stream-K (sk_iters > 0): sk_iters steps starting at (cta * sk_iters), crossing tile boundaries;
