@@ -79,6 +79,14 @@ __device__ __forceinline__ float max_halves(float x) {
   swap_halves(x, lo, hi);
   return fmaxf(lo, hi);
 }
+// max_halves with the max inside the asm: on the asm's outputs fmaxf first canonicalises each operand (two
+// extra VALU); v_max_f32 of the two halves is the same value for every non-NaN input
+__device__ __forceinline__ float max_halves_fused(float x) {
+  float lo = x, hi = x, r;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %1, %2\n\ts_nop 1\n\tv_max_f32 %0, %1, %2"
+               : "=v"(r), "+v"(lo), "+v"(hi));
+  return r;
+}
 __device__ __forceinline__ float sum_halves(float x) {
   float lo, hi;
   swap_halves(x, lo, hi);
@@ -107,15 +115,21 @@ __device__ __forceinline__ int vt_off(int d, int kq) {
 }
 
 // NW waves x 32 queries per workgroup: 4 (two workgroups per CU) or 8 (one per CU; each K / V tile staged in
-// LDS then feeds twice the MFMA work)
-template <int DT, bool GATE, bool BIG, bool CAUSAL, int NW>
+// LDS then feeds twice the MFMA work).
+// AA: the scalar-address form. Wave-uniform values (wave index, LDS stage offsets, K / V block bases) are read
+// into scalars; K / V loads of a full block are a scalar base plus per-lane 32-bit offsets computed once (only
+// a block reaching past Lk clamps its rows); the V^T transpose writes and operand reads take four per-lane
+// offsets each, computed once; the block max of the two lane halves runs inside the lane-swap asm. The same
+// values land in the same places: results are bitwise those of the default form. Needs ldk, ldv <= 2^24.
+template <int DT, bool GATE, bool BIG, bool CAUSAL, int NW, bool AA = false>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_kernel(AttnArgs p) {
   constexpr int BQ = 32 * NW;
   // [K stage 0 | K stage 1 | V^T stage 0 | 1 | 2]
   __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];
   typedef __attribute__((address_space(3))) void lds_void;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = AA ? __builtin_amdgcn_readfirstlane(tid >> 6) : tid >> 6;
   const int l32 = lane & 31, hh = lane >> 5;
   // Workgroup -> (head, query block). The dispatcher deals workgroups round-robin to the 8 XCDs (each
   // with its own L2); ids are remapped so that each XCD walks whole heads in order: its resident
@@ -149,14 +163,42 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_kernel(AttnArgs p) {
   // ---- K tile DMA: instruction r of wave w fills 1 KB = rows 4 (4 r + w) .. +3; lane -> row lane / 16,
   //      chunk slot lane & 15 receives logical chunk (lane & 15) ^ (row & 15) ----
   const uint16_t* kbase = (const uint16_t*)p.K + kvh * D;
-  auto issue_k = [&](int b, int buf) {
+  // AA: per-lane 32-bit byte offsets of the K rows within a block (64 rows x ldk x 2 B < 2^31)
+  uint32_t koff[16 / NW];
+  if constexpr (AA) {
 #pragma unroll
     for (int r = 0; r < 16 / NW; r++) {
       const int row = 4 * (NW * r + wave) + (lane >> 4);
-      const int key = min(b * BKEYS + row, p.Lk - 1);
-      const int c = (lane & 15) ^ (row & 15);
-      __builtin_amdgcn_global_load_lds((const void*)(kbase + (size_t)key * p.ldk + c * 8),
-                                       (lds_void*)(lds + buf * KT_BYTES + (NW * r + wave) * 1024), 16, 0, 0);
+      koff[r] = (uint32_t)(row * p.ldk + ((lane & 15) ^ (row & 15)) * 8) * 2u;
+    }
+  }
+  auto issue_k = [&](int b, int buf) {
+    if constexpr (AA) {
+      const char* kblk = (const char*)kbase + (size_t)b * BKEYS * p.ldk * 2;
+      if (b * BKEYS + BKEYS <= p.Lk) {
+#pragma unroll
+        for (int r = 0; r < 16 / NW; r++)
+          __builtin_amdgcn_global_load_lds((const void*)(kblk + koff[r]),
+                                           (lds_void*)(lds + buf * KT_BYTES + (NW * r + wave) * 1024), 16, 0, 0);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16 / NW; r++) {
+          const int row = 4 * (NW * r + wave) + (lane >> 4);
+          const int krel = min(row, p.Lk - 1 - b * BKEYS);
+          const int c = (lane & 15) ^ (row & 15);
+          __builtin_amdgcn_global_load_lds((const void*)(kblk + (size_t)(krel * p.ldk + c * 8) * 2),
+                                           (lds_void*)(lds + buf * KT_BYTES + (NW * r + wave) * 1024), 16, 0, 0);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16 / NW; r++) {
+        const int row = 4 * (NW * r + wave) + (lane >> 4);
+        const int key = min(b * BKEYS + row, p.Lk - 1);
+        const int c = (lane & 15) ^ (row & 15);
+        __builtin_amdgcn_global_load_lds((const void*)(kbase + (size_t)key * p.ldk + c * 8),
+                                         (lds_void*)(lds + buf * KT_BYTES + (NW * r + wave) * 1024), 16, 0, 0);
+      }
     }
   };
   // ---- V tile: thread -> keys 4 vkq .. 4 vkq + 3, dims 8 vc .. 8 vc + 7. Within a wave the four 16-lane
@@ -165,20 +207,47 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_kernel(AttnArgs p) {
   const int vlane = tid & 63;
   const int vkq = 4 * (wave & 3) + (((vlane >> 4) & 1) << 1 | ((vlane >> 5) & 1)), vc = vlane & 15;
   const uint16_t* vbase = (const uint16_t*)p.V + kvh * D + vc * 8;
+  const uint32_t voff0 = (uint32_t)(4 * vkq * p.ldv) * 2u;  // AA: this lane's first V row in a block (bytes)
   u32x4 vr[4];
   auto load_v = [&](int b) {
+    if constexpr (AA) {
+      const char* vblk = (const char*)vbase + (size_t)b * BKEYS * p.ldv * 2;
+      if (b * BKEYS + BKEYS <= p.Lk) {
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int key = min(b * BKEYS + 4 * vkq + r, p.Lk - 1);
-      vr[r] = *(const u32x4*)(vbase + (size_t)key * p.ldv);
+        for (int r = 0; r < 4; r++) vr[r] = *(const u32x4*)(vblk + (size_t)r * p.ldv * 2 + voff0);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const int krel = min(4 * vkq + r, p.Lk - 1 - b * BKEYS);
+          vr[r] = *(const u32x4*)(vblk + (size_t)krel * p.ldv * 2);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int key = min(b * BKEYS + 4 * vkq + r, p.Lk - 1);
+        vr[r] = *(const u32x4*)(vbase + (size_t)key * p.ldv);
+      }
     }
   };
   // 8 dims x 4 keys: V^T[d][4 vkq .. 4 vkq + 3] as one 8-byte write per d. Write i covers dim
   // 8 vc + (i ^ (vc & 1)): odd-vc lanes swap the two dims of each dword, which only changes the v_perm
   // selector, and spreads the half wave's writes over both row parities.
   const uint32_t sel_lo = (vc & 1) ? 0x07060302u : 0x05040100u, sel_hi = (vc & 1) ? 0x05040100u : 0x07060302u;
+  // AA: write i goes to vt_off(8 vc + (i ^ q), vkq), q = vc & 1. The row swizzle of dims 8 vc + j is
+  // sw1 ^ (j >> 1) with sw1 = 4 q ^ ((vc >> 1) & 7), so that offset is vst[i >> 1] for even i and
+  // vst[i >> 1] + 128 - 256 q for odd i: four per-lane values, computed once.
+  uint32_t vst[4];
+  const int vdelta = 128 - 256 * (vc & 1);
+  if constexpr (AA) {
+    const int X = (2 * (vkq >> 2) + (vkq & 1)) ^ (4 * (vc & 1)) ^ ((vc >> 1) & 7);
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+      vst[t] = 1024 * vc + ((vkq >> 1) & 1) * 8 + 256 * t + 16 * (X ^ t) + 128 * (vc & 1);
+  }
   auto store_vt = [&](int buf) {
-    char* vt = lds + K_STAGES * KT_BYTES + buf * VT_BYTES;
+    char* vt = lds + (AA ? __builtin_amdgcn_readfirstlane(K_STAGES * KT_BYTES + buf * VT_BYTES)
+                         : K_STAGES * KT_BYTES + buf * VT_BYTES);
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       const int d = vc * 8 + (i ^ (vc & 1));
@@ -186,7 +255,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_kernel(AttnArgs p) {
       const uint32_t sel = (i & 1) ? sel_hi : sel_lo;
       const uint32_t lo = __builtin_amdgcn_perm(vr[1][w], vr[0][w], sel);  // keys 4vkq, 4vkq+1 of dim d
       const uint32_t hi = __builtin_amdgcn_perm(vr[3][w], vr[2][w], sel);  // keys 4vkq+2, 4vkq+3
-      *(u32x2*)(vt + vt_off(d, vkq)) = (u32x2){lo, hi};
+      const uint32_t off = AA ? vst[i >> 1] + ((i & 1) ? vdelta : 0) : (uint32_t)vt_off(d, vkq);
+      *(u32x2*)(vt + off) = (u32x2){lo, hi};
     }
   };
   // kb of keys 32 kh + l32 of block b (lanes of k-slice 1 hold 0), loaded one block ahead
@@ -203,16 +273,27 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_kernel(AttnArgs p) {
   for (int db = 0; db < 4; db++) o[db] = (f32x16){};
   float m = M_INIT, l = 0.f;
 
-  // O^T += V^T P^T of one block: P^T from registers, V^T from its LDS stage
+  // O^T += V^T P^T of one block: P^T from registers, V^T from its LDS stage. AA: the operand of (db, j) is
+  // vt_off(32 db + l32, 4 j + hh) = 4096 db + voff[j ^ db]: for d = 32 db + l32 the swizzle is sw0 ^ 2 db with
+  // sw0 = ((l32 >> 1) ^ (l32 >> 4)) & 7, and XOR by 2 db moves chunk 2 j + hh to 2 (j ^ db) + hh. Four
+  // per-lane offsets then serve all 16 reads, with 4096 db as the immediate.
+  uint32_t voff[4];
+  if constexpr (AA) {
+    const int sw0 = ((l32 >> 1) ^ (l32 >> 4)) & 7;
+#pragma unroll
+    for (int t = 0; t < 4; t++) voff[t] = l32 * 128 + 16 * ((2 * t + hh) ^ sw0);
+  }
   auto pv = [&](const u32x4 (&pf)[4], int vbuf) {
-    const char* vt = lds + K_STAGES * KT_BYTES + vbuf * VT_BYTES;
+    const char* vt = lds + (AA ? __builtin_amdgcn_readfirstlane(K_STAGES * KT_BYTES + vbuf * VT_BYTES)
+                               : K_STAGES * KT_BYTES + vbuf * VT_BYTES);
 #pragma unroll
     for (int db = 0; db < 4; db++) {
       const int d = db * 32 + l32;
 #pragma unroll
       for (int j = 0; j < 4; j++) {
         // operand slots 0..3: key quad 4 j + hh, slots 4..7: quad 4 j + 2 + hh (one chunk, see vt_off)
-        const u32x4 vf = *(const u32x4*)(vt + vt_off(d, 4 * j + hh));
+        const uint32_t off = AA ? voff[j ^ db] + db * 4096 : (uint32_t)vt_off(d, 4 * j + hh);
+        const u32x4 vf = *(const u32x4*)(vt + off);
         o[db] = mfma32<DT>(vf, pf[j], o[db]);
       }
     }
@@ -238,7 +319,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_kernel(AttnArgs p) {
       issue_k(b + 1, (b + 1) & 1);
       if (wave < 4) load_v(b + 1);
     }
-    const char* kt = lds + (b & 1) * KT_BYTES;
+    const char* kt = lds + (AA ? __builtin_amdgcn_readfirstlane((b & 1) * KT_BYTES) : (b & 1) * KT_BYTES);
 
     // S^T = K Q^T: st[kh] holds keys 32 kh + 8 (i / 4) + 4 hh + i % 4 (i = 0..15) of query q
     f32x16 st[2];
@@ -269,7 +350,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_kernel(AttnArgs p) {
         st[kh][i] = s;
         bmax = fmaxf(bmax, s);
       }
-    bmax = max_halves(bmax) * p.scale_log2;
+    bmax = (AA ? max_halves_fused(bmax) : max_halves(bmax)) * p.scale_log2;
     // lazy max update (log2 units): only when some query of the wave grew by more than LAZY_TH (O then
     // already holds block b - 1); the condition is wave-uniform and read into a scalar so the rescale
     // stays a branch
@@ -335,25 +416,39 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_kernel(AttnArgs p) {
     }
 }
 
-template <int DT, bool GATE, bool BIG, int NW>
-hipError_t launch4(bool causal, const AttnArgs& a, hipStream_t st) {
+template <int DT, bool GATE, bool BIG, int NW, bool AA>
+hipError_t launch5(bool causal, const AttnArgs& a, hipStream_t st) {
   dim3 grid(((a.Lq + 32 * NW - 1) / (32 * NW)) * a.heads), block(64 * NW);
   if (causal)
-    hipLaunchKernelGGL((attn_kernel<DT, GATE, BIG, true, NW>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((attn_kernel<DT, GATE, BIG, true, NW, AA>), grid, block, 0, st, a);
   else
-    hipLaunchKernelGGL((attn_kernel<DT, GATE, BIG, false, NW>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((attn_kernel<DT, GATE, BIG, false, NW, AA>), grid, block, 0, st, a);
   return hipGetLastError();
 }
 
+template <int DT, bool GATE, bool BIG, int NW>
+hipError_t launch4(bool causal, bool aa, const AttnArgs& a, hipStream_t st) {
+  return aa ? launch5<DT, GATE, BIG, NW, true>(causal, a, st) : launch5<DT, GATE, BIG, NW, false>(causal, a, st);
+}
+
 template <int DT, bool GATE, bool BIG>
-hipError_t launch3(bool causal, int nw, const AttnArgs& a, hipStream_t st) {
-  return nw == 8 ? launch4<DT, GATE, BIG, 8>(causal, a, st) : launch4<DT, GATE, BIG, 4>(causal, a, st);
+hipError_t launch3(bool causal, bool aa, int nw, const AttnArgs& a, hipStream_t st) {
+  return nw == 8 ? launch4<DT, GATE, BIG, 8>(causal, aa, a, st) : launch4<DT, GATE, BIG, 4>(causal, aa, a, st);
 }
 
 template <int DT>
-hipError_t launch2(bool gate, bool big, bool causal, int nw, const AttnArgs& a, hipStream_t st) {
-  if (gate) return big ? launch3<DT, true, true>(causal, nw, a, st) : launch3<DT, true, false>(causal, nw, a, st);
-  return big ? launch3<DT, false, true>(causal, nw, a, st) : launch3<DT, false, false>(causal, nw, a, st);
+hipError_t launch2(bool gate, bool big, bool causal, bool aa, int nw, const AttnArgs& a, hipStream_t st) {
+  if (gate)
+    return big ? launch3<DT, true, true>(causal, aa, nw, a, st) : launch3<DT, true, false>(causal, aa, nw, a, st);
+  return big ? launch3<DT, false, true>(causal, aa, nw, a, st) : launch3<DT, false, false>(causal, aa, nw, a, st);
+}
+
+// KH_ATTN_ADDR=1 selects the scalar-address form (attn_kernel AA), bitwise the same results; it needs K / V
+// row strides of at most 2^24 elements (per-lane 32-bit offsets within a 64-key block) and the default form
+// runs otherwise (read per call)
+bool attn_addr(int ldk, int ldv) {
+  const char* e = getenv("KH_ATTN_ADDR");
+  return e && e[0] == '1' && e[1] == 0 && ldk <= (1 << 24) && ldv <= (1 << 24);
 }
 
 // Waves per workgroup: 8 (measured at 4608 tokens: 24 heads 400 -> 324 us; 48 q / 12 kv heads + gate 645 ->
@@ -386,8 +481,9 @@ int attention(hipStream_t st, const void* Q, const void* K, const void* V, void*
   AttnArgs a{Q, K, V, O, G, QB, KB, Lq, Lk, heads, ldq, ldk, ldv, ldo, group, q_pos0, ldg, heads, kv_heads,
              (float)(1.4426950408889634 / 11.313708498984761)};
   const int nw = attn_waves(QB != nullptr);
-  const hipError_t r = dtype == KH_F16 ? launch2<KH_F16>(G != nullptr, QB != nullptr, causal != 0, nw, a, st)
-                                       : launch2<KH_BF16>(G != nullptr, QB != nullptr, causal != 0, nw, a, st);
+  const bool aa = attn_addr(ldk, ldv);
+  const hipError_t r = dtype == KH_F16 ? launch2<KH_F16>(G != nullptr, QB != nullptr, causal != 0, aa, nw, a, st)
+                                       : launch2<KH_BF16>(G != nullptr, QB != nullptr, causal != 0, aa, nw, a, st);
   if (r != hipSuccess) return e.hip(r, "attention launch");
   return KH_OK;
 }
