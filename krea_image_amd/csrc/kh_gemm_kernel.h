@@ -674,8 +674,28 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
 
   const int out_n0 = (EPI == KH_EPI_SWIGLU) ? n0 / 2 : n0;
   const int out_N = (EPI == KH_EPI_SWIGLU) ? p.N / 2 : p.N;
+  // copy-out geometry: 16-byte chunks, CPR per staged row, consecutive threads along a row
+  constexpr int CPR = OUT_COLS * ELEM / 16;
+  constexpr int CHUNKS = PASS_ROWS * CPR;
+  // WA = 3, residual epilogues: every residual chunk this thread will update in a pass is loaded before the
+  // pass stages its tile, so the loads' latency overlaps the staging instead of following it four chunks at
+  // a time (the same values are added in the same order: results are bitwise equal)
+  constexpr bool RPF = WA == 3 && (EPI == KH_EPI_RESID || EPI == KH_EPI_RESID_GATE) && !CONV;
+  constexpr int RPF_N = RPF ? (CHUNKS + NTHR - 1) / NTHR : 1;
+  f32x4 xpre[RPF_N];
 #pragma unroll
   for (int pass = 0; pass < BM / PASS_ROWS; pass++) {
+    if constexpr (RPF) {
+      const int grow0 = m0 + pass * PASS_ROWS;
+#pragma unroll
+      for (int i = 0; i < RPF_N; i++) {
+        const int idx = tid + i * NTHR;
+        const int r = idx / CPR, c = idx % CPR;
+        const int gm_ = grow0 + r, gcol = out_n0 + c * (16 / ELEM);
+        if (idx < CHUNKS && gm_ < p.M && gcol < out_N)
+          xpre[i] = *(const f32x4*)((const char*)p.C + ((size_t)gm_ * p.ldc + gcol) * ELEM);
+      }
+    }
     if (PASS_ROWS == BM || (wm * C_::WME) / PASS_ROWS == pass) {
       const int row_base = wm * C_::WME - pass * PASS_ROWS;
 #pragma unroll
@@ -712,10 +732,18 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmArgs p) {
       }
     }
     lds_barrier();
-    // copy-out: 16-byte chunks, CPR per staged row, consecutive threads along a row
-    constexpr int CPR = OUT_COLS * ELEM / 16;
-    constexpr int CHUNKS = PASS_ROWS * CPR;
     const int grow0 = m0 + pass * PASS_ROWS;
+    if constexpr (RPF) {
+#pragma unroll
+      for (int i = 0; i < RPF_N; i++) {
+        const int idx = tid + i * NTHR;
+        const int r = idx / CPR, c = idx % CPR;
+        const int gm_ = grow0 + r, gcol = out_n0 + c * (16 / ELEM);
+        if (idx >= CHUNKS || gm_ >= p.M || gcol >= out_N) continue;
+        const f32x4 v = *(const f32x4*)(lds + r * ROW_BYTES + c * 16);
+        *(f32x4*)((char*)p.C + ((size_t)gm_ * p.ldc + gcol) * ELEM) = xpre[i] + v;
+      }
+    } else
 #pragma unroll 4
     for (int idx = tid; idx < CHUNKS; idx += NTHR) {
       const int r = idx / CPR, c = idx % CPR;
