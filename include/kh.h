@@ -71,6 +71,8 @@ typedef struct kh_weight {
  * 256-wide tiles fill only part of one wave of workgroups and 192-wide ones still fit in one (4096 x 3072);
  * 256 x 128 for 16-bit weights where N pads less to 128 (e.g. 64, 128). KH_GEMM_TN192=0 keeps 256-wide
  * tiles. Every tile width sums each output's products in the same order: the results are bitwise equal.
+ * KH_GEMM_WAHEAD=3 loads packed per-channel int8 weights three K steps ahead instead of two (data-parallel
+ * launches; bitwise the same results).
  * Replaces krea::Metal::gemm (engine/src/metal.h:66-69, engine/src/metal.mm:146-163). */
 int kh_gemm(kh_stream stream, int epi, const void* A, int a_dtype, const kh_weight* W, void* C, int M, int N, int K,
             int lda, int ldw, int ldc, const void* vec, char* err, int errlen);
@@ -126,7 +128,8 @@ int kh_pack_int8(kh_stream stream, const void* W, int K, int ldw, void* out, cha
  * column 128 h (kv head at 128 (h / group)). causal: key k visible to query i iff k <= i + q_pos0. QB [Lq, heads]
  * and KB [Lk, heads / group] (f32, both or neither): the rank-1 score term of a "big" head dimension.
  * Workgroups of 8 x 32 queries (4 x 32 with the rank-1 term; KH_ATTN_WAVES=4 / 8 overrides); either size
- * computes the same per-query arithmetic.
+ * computes the same per-query arithmetic. KH_ATTN_ADDR=1 selects the kernel's scalar-address form (bitwise the
+ * same results; used when ldk, ldv <= 2^24).
  * Replaces krea::Metal::attention (engine/src/metal.h:86-88, engine/src/metal.mm:193-202). */
 int kh_attention(kh_stream stream, const void* Q, const void* K, const void* V, void* O, int dtype, int Lq, int Lk,
                  int heads, int ldq, int ldk, int ldv, int ldo, int group, int causal, int q_pos0, const void* G,
